@@ -1,0 +1,80 @@
+/*
+ * kda.h -- C ABI of the MI355X (gfx950) operator library.
+ *
+ * One entry point per operator of the reference's NKIBench operator set.  Each
+ * replaces the NKI `kernel(...)` that the reference's adapter assembles and its
+ * profiler runs (adapter/nkibench_case.py:105-166, `kernel_fn="kernel"` :177);
+ * the argument order follows the reference kernel's HBM-tensor order, which is
+ * the order of the numpy `forward(...)` parameters (adapter/nkibench_case.py:199-216).
+ *
+ * Conventions (all entry points):
+ *   - Every pointer is a device pointer the caller owns (allocated with hipMalloc
+ *     or by PyTorch).  The library never allocates, frees or retains them.
+ *   - Tensors are dense and row-major in the "natural" layout of the numpy
+ *     reference (every NKIBench transform_to_nki_inputs is a pure reshape).
+ *   - bf16 tensors are passed as `kda_bf16*` (raw 16-bit storage, IEEE bfloat16).
+ *   - `stream` is a hipStream_t cast to void*; NULL means the default stream.
+ *     Launches are asynchronous; no entry point synchronises the host.
+ *   - Return value: KDA_OK (0) on success, otherwise a KDA_ERR_* code; the
+ *     message for the last failure on the calling thread is kda_last_error().
+ *     Nothing is launched when a call fails argument validation.
+ */
+#ifndef KDA_H_
+#define KDA_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t kda_bf16;
+
+enum {
+  KDA_OK = 0,
+  KDA_ERR_INVALID_ARG = 1,  /* null pointer, bad size, misaligned pointer       */
+  KDA_ERR_UNSUPPORTED = 2,  /* shape outside what the kernel was written for    */
+  KDA_ERR_HIP = 3           /* a HIP runtime call failed (launch, attribute...) */
+};
+
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int kda_version(void);
+
+/* Message describing the most recent failure on the calling thread ("" if none). */
+const char* kda_last_error(void);
+
+/* ---------------------------------------------------------------- elementwise */
+
+/* SiLU, y = x / (1 + exp(-x)), fp32, n elements.
+ * Replaces kernel(v1) of workspaces/silu/runs/silu_v3_s7.py:31-71
+ * (forward `y = x/(1+exp(-x))`, prompts/_gen_prompts.py:25).  x and y may alias. */
+int kda_silu_f32(const float* x, float* y, int64_t n, void* stream);
+
+/* AdamW step (decoupled weight decay), fp32, n elements:
+ *   p' = p*(1 - lr*wd);  m' = b1*m + (1-b1)*g;  v' = b2*v + (1-b2)*g*g
+ *   p'' = p' - (lr/(1-b1^step)) * m' / (sqrt(v')/sqrt(1-b2^step) + eps)
+ * Reads param_in/grad/m_in/v_in; writes param_out (may equal param_in for the
+ * in-place step) and, when non-NULL, m_out / v_out (may equal m_in / v_in).
+ * Replaces kernel(v1..v4) = (theta, g, m, v) of workspaces/adamw/runs/adamw_v1.py:50-97,
+ * whose forward is this update at step 1, lr 1e-3, wd 1e-2, eps 1e-8
+ * (workspaces/adamw/docs/draft-phase1.md:20-26) returning only the new theta. */
+int kda_adamw_f32(const float* param_in, const float* grad, const float* m_in,
+                  const float* v_in, float* param_out, float* m_out, float* v_out,
+                  int64_t n, float lr, float beta1, float beta2, float eps,
+                  float weight_decay, int64_t step, void* stream);
+
+/* Half-split rotary embedding applied along axis 0 of x (D rows, S columns):
+ *   out[d]       = x[d]*cos[d] - x[d+D/2]*sin[d]        d < D/2
+ *   out[d + D/2] = x[d]*sin[d] + x[d+D/2]*cos[d]
+ * x, out: (D, S) fp32; cos, sin: (D/2, S) fp32; D even.  Rounded exactly like the
+ * numpy reference (two products, then one add/sub; no fused multiply-add).
+ * Replaces kernel(x_in, cos, sin) of
+ * workspaces/rope_single_freq_apply/runs/rope_v1.py:32-80. */
+int kda_rope_f32(const float* x, const float* cos_t, const float* sin_t, float* out,
+                 int64_t d, int64_t s, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KDA_H_ */

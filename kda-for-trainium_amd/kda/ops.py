@@ -1,0 +1,135 @@
+"""One Python callable per operator, backed by the gfx950 kernels in libkda.so.
+
+Each callable takes the natural-layout tensors that the reference's adapter
+hands to numpy ``forward(...)`` -- keyword names are forward()'s parameter
+names (adapter/nkibench_case.py:147-155, 199-216) -- and returns the output
+tensor, allocated on the inputs' device.  Inputs must be contiguous CUDA (ROCm)
+tensors of the stated dtype; anything else raises ValueError before any launch.
+Every kernel runs on the current torch stream of the inputs' device.  There is
+no CPU or PyTorch fallback: without libkda.so these functions raise.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "silu",
+    "adamw",
+    "adamw_step_",
+    "rope_single_freq_apply",
+]
+
+
+# ----------------------------------------------------------------- helpers
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _check(name: str, t: torch.Tensor, dtype: torch.dtype,
+           shape: Optional[Sequence[int]] = None, ndim: Optional[int] = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name}: expected a torch.Tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: must be a GPU tensor (got device {t.device})")
+    if t.dtype != dtype:
+        raise ValueError(f"{name}: expected dtype {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name}: expected {ndim} dims, got shape {tuple(t.shape)}")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name}: expected shape {tuple(shape)}, got {tuple(t.shape)}")
+
+
+def _same_device(*ts: torch.Tensor) -> None:
+    dev = ts[0].device
+    for t in ts[1:]:
+        if t.device != dev:
+            raise ValueError(f"all tensors must be on one device ({dev} vs {t.device})")
+
+
+# ----------------------------------------------------------------- elementwise
+
+def silu(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = x / (1 + exp(-x)), fp32, any shape.
+
+    Reference: workspaces/silu/runs/silu_v3_s7.py:31-71 (kernel(v1)); forward
+    ``y = x/(1+exp(-x))`` per prompts/_gen_prompts.py:25.
+    """
+    _check("x", x, torch.float32)
+    if out is None:
+        out = torch.empty_like(x)
+    else:
+        _check("out", out, torch.float32, shape=x.shape)
+        _same_device(x, out)
+    _lib.call("kda_silu_f32", x.data_ptr(), out.data_ptr(), x.numel(), _stream(x))
+    return out
+
+
+def adamw(theta: torch.Tensor, g: torch.Tensor, m: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """NKIBench AdamW forward: returns the new theta, leaves m and v untouched.
+
+    ``theta_t = theta - 1e-5*theta; m_t = 0.9m + 0.1g; v_t = 0.999v + 0.001g^2;
+    new = theta_t - 0.01*m_t/(sqrt(1000*v_t) + 1e-8)`` -- i.e. one decoupled-
+    weight-decay Adam step at step 1 with lr 1e-3, weight decay 1e-2, eps 1e-8
+    (workspaces/adamw/docs/draft-phase1.md:20-26; kernel(v1..v4) =
+    (theta, g, m, v) of workspaces/adamw/runs/adamw_v1.py:50-97).
+    """
+    for name, t in (("theta", theta), ("g", g), ("m", m), ("v", v)):
+        _check(name, t, torch.float32, shape=theta.shape)
+    _same_device(theta, g, m, v)
+    out = torch.empty_like(theta)
+    _lib.call("kda_adamw_f32", theta.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(),
+              out.data_ptr(), None, None, theta.numel(),
+              1e-3, 0.9, 0.999, 1e-8, 1e-2, 1, _stream(theta))
+    return out
+
+
+def adamw_step_(param: torch.Tensor, grad: torch.Tensor, m: torch.Tensor, v: torch.Tensor,
+                lr: float = 1e-3, beta1: float = 0.9, beta2: float = 0.999, eps: float = 1e-8,
+                weight_decay: float = 1e-2, step: int = 1) -> torch.Tensor:
+    """In-place fused AdamW step over flat fp32 buffers; updates param, m, v.
+
+    Same update as torch.optim.AdamW (non-amsgrad, maximize=False) at the given
+    step count: ``p *= 1-lr*wd; m = b1*m+(1-b1)*g; v = b2*v+(1-b2)*g^2;
+    p -= lr/(1-b1^step) * m / (sqrt(v)/sqrt(1-b2^step) + eps)``.  One pass:
+    reads p, g, m, v and writes p, m, v (28 bytes per element).
+    """
+    for name, t in (("param", param), ("grad", grad), ("m", m), ("v", v)):
+        _check(name, t, torch.float32, shape=param.shape)
+    _same_device(param, grad, m, v)
+    if int(step) < 1:
+        raise ValueError(f"step must be >= 1, got {step}")
+    _lib.call("kda_adamw_f32", param.data_ptr(), grad.data_ptr(), m.data_ptr(), v.data_ptr(),
+              param.data_ptr(), m.data_ptr(), v.data_ptr(), param.numel(),
+              float(lr), float(beta1), float(beta2), float(eps), float(weight_decay), int(step),
+              _stream(param))
+    return param
+
+
+def rope_single_freq_apply(x_in: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Half-split RoPE along axis 0: x_in (D, S), cos/sin (D/2, S), fp32.
+
+    ``out[:D/2] = x0*cos - x1*sin; out[D/2:] = x0*sin + x1*cos`` with
+    x0 = x_in[:D/2], x1 = x_in[D/2:] (workspaces/rope_single_freq_apply/docs/
+    draft-phase1.md:18-27; kernel(x_in, cos, sin) of
+    workspaces/rope_single_freq_apply/runs/rope_v1.py:32-80).  Bit-identical to
+    the numpy reference (no fused multiply-add).
+    """
+    _check("x_in", x_in, torch.float32, ndim=2)
+    d, s = x_in.shape
+    if d % 2:
+        raise ValueError(f"x_in: head dim {d} must be even")
+    _check("cos", cos, torch.float32, shape=(d // 2, s))
+    _check("sin", sin, torch.float32, shape=(d // 2, s))
+    _same_device(x_in, cos, sin)
+    out = torch.empty_like(x_in)
+    _lib.call("kda_rope_f32", x_in.data_ptr(), cos.data_ptr(), sin.data_ptr(), out.data_ptr(),
+              d, s, _stream(x_in))
+    return out

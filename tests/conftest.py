@@ -1,0 +1,47 @@
+"""Shared pytest setup: import paths, the `gpu` marker, GPU helpers."""
+import os
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+PKG_DIR = ROOT / "kda-for-trainium_amd"
+for p in (str(ROOT), str(PKG_DIR)):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs through libkda.so on cuda:0)")
+
+
+def _have_gpu() -> bool:
+    try:
+        import torch
+        return torch.cuda.is_available()
+    except Exception:
+        return False
+
+
+def pytest_collection_modifyitems(config, items):
+    if _have_gpu():
+        return
+    skip = pytest.mark.skip(reason="no GPU in this environment")
+    for item in items:
+        if "gpu" in item.keywords:
+            item.add_marker(skip)
+
+
+@pytest.fixture(scope="session")
+def dev():
+    import torch
+    return torch.device("cuda", 0)
+
+
+@pytest.fixture(autouse=True)
+def _announce(request):
+    # Name the case before any GPU work so a hang or fault is attributable.
+    if "gpu" in request.keywords:
+        print(f"\n[gpu-test] {request.node.nodeid}", flush=True)
+    yield

@@ -1,0 +1,61 @@
+"""The C ABI: libkda.so loads, exports every symbol include/kda.h declares, the
+ctypes table matches the header, and argument validation fails cleanly.  CPU only:
+the calls below are rejected before any HIP call is made."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from kda import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "kda.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(kda_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    assert "kda_version" in names and "kda_last_error" in names and len(names) >= 5
+
+
+def test_library_exports_every_declared_symbol():
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (kda_\w+)", out))
+    missing = [n for n in declared_functions() if n not in exported]
+    assert not missing, missing
+
+
+def test_ctypes_table_matches_header():
+    header = set(declared_functions()) - {"kda_version", "kda_last_error"}
+    assert header == set(_lib.SIGNATURES), header ^ set(_lib.SIGNATURES)
+
+
+def test_version_and_load():
+    assert _lib.version() == 100
+    assert _lib.lib().kda_last_error() == b""
+
+
+def test_invalid_arguments_rejected_without_launch():
+    with pytest.raises(ValueError, match="n=-1"):
+        _lib.call("kda_silu_f32", None, None, -1, None)
+    with pytest.raises(ValueError, match="even D"):
+        _lib.call("kda_rope_f32", None, None, None, None, 3, 8, None)
+    with pytest.raises(ValueError, match="step"):
+        _lib.call("kda_adamw_f32", None, None, None, None, None, None, None, 8,
+                  1e-3, 0.9, 0.999, 1e-8, 0.0, 0, None)
+    with pytest.raises(ValueError, match="null pointer"):
+        _lib.call("kda_silu_f32", None, None, 16, None)
+
+
+def test_ops_reject_cpu_tensors():
+    import torch
+    from kda import ops
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.silu(torch.zeros(4))
