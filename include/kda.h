@@ -73,6 +73,32 @@ int kda_adamw_f32(const float* param_in, const float* grad, const float* m_in,
 int kda_rope_f32(const float* x, const float* cos_t, const float* sin_t, float* out,
                  int64_t d, int64_t s, void* stream);
 
+/* ---------------------------------------------------------------- bf16 GEMMs
+ * bf16 storage, fp32 accumulation on MFMA, bf16 output.  Shape limits: K and N
+ * multiples of 8 (16-byte rows); all pointers 16-byte aligned; any M. */
+
+/* c[M,N] = a[M,K] @ b[K,N].  The GEMM core of workspaces/matmul/runs/matmul_v1.py:10-111
+ * (kernel(v1=lhs, v2=rhs)), at bf16 precision. */
+int kda_matmul_bf16(const kda_bf16* a, const kda_bf16* b, kda_bf16* c, int64_t m, int64_t k,
+                    int64_t n, void* stream);
+
+/* y[M,N] = (x * rsqrt(mean_k(x^2) + eps) * gamma) @ w, x [M,K], gamma [K] (8-byte
+ * aligned), w [K,N].  RMSNorm fused into the GEMM: one kernel, x read once per tile.
+ * Replaces kernel(v1=x, v2=w) of workspaces/rmsnorm_matmul/runs/rmsnorm_matmul_v1.py:10-138
+ * (which has no gain and no eps) and the x+z-free part of
+ * workspaces/add_rmsnorm_matmul/runs/add_rmsnorm_matmul_v1.py:8-146 (gain g, eps). */
+int kda_rmsnorm_matmul_bf16(const kda_bf16* x, const kda_bf16* gamma, const kda_bf16* w,
+                            kda_bf16* y, int64_t m, int64_t k, int64_t n, float eps,
+                            void* stream);
+
+/* y[M,K] = (silu(x @ w_gate) * (x @ w_up)) @ w_down with x [M,K], w_up/w_gate [K,F],
+ * w_down [F,K].  h is caller-provided scratch of M*F bf16 (the gated activation,
+ * written by the first kernel and read by the second).  Argument order follows
+ * kernel(v1=x, v2=w_up, v3=w_down, v4=w_gate) of workspaces/swiglu/runs/swiglu_v1.py:38-146. */
+int kda_swiglu_bf16(const kda_bf16* x, const kda_bf16* w_up, const kda_bf16* w_down,
+                    const kda_bf16* w_gate, kda_bf16* h, kda_bf16* y, int64_t m, int64_t k,
+                    int64_t f, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

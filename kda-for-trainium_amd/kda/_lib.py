@@ -27,6 +27,9 @@ SIGNATURES = {
     "kda_silu_f32": [_p, _p, _i64, _p],
     "kda_adamw_f32": [_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _f32, _f32, _f32, _f32, _i64, _p],
     "kda_rope_f32": [_p, _p, _p, _p, _i64, _i64, _p],
+    "kda_matmul_bf16": [_p, _p, _p, _i64, _i64, _i64, _p],
+    "kda_rmsnorm_matmul_bf16": [_p, _p, _p, _p, _i64, _i64, _i64, _f32, _p],
+    "kda_swiglu_bf16": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
 }
 
 

@@ -22,7 +22,13 @@ __all__ = [
     "adamw",
     "adamw_step_",
     "rope_single_freq_apply",
+    "matmul",
+    "rmsnorm_matmul",
+    "swiglu",
 ]
+
+BF16 = torch.bfloat16
+F32 = torch.float32
 
 
 # ----------------------------------------------------------------- helpers
@@ -132,4 +138,87 @@ def rope_single_freq_apply(x_in: torch.Tensor, cos: torch.Tensor, sin: torch.Ten
     out = torch.empty_like(x_in)
     _lib.call("kda_rope_f32", x_in.data_ptr(), cos.data_ptr(), sin.data_ptr(), out.data_ptr(),
               d, s, _stream(x_in))
+    return out
+
+
+# ----------------------------------------------------------------- GEMM family
+
+def _gemm_dims(name_a: str, a: torch.Tensor, name_b: str, b: torch.Tensor):
+    if a.dim() != 2 or b.dim() != 2:
+        raise ValueError(f"{name_a}, {name_b}: expected 2-D tensors, got {tuple(a.shape)}, {tuple(b.shape)}")
+    if a.shape[1] != b.shape[0]:
+        raise ValueError(f"inner dims differ: {name_a} {tuple(a.shape)} vs {name_b} {tuple(b.shape)}")
+    return a.shape[0], a.shape[1], b.shape[1]
+
+
+def matmul(lhs: torch.Tensor, rhs: torch.Tensor) -> torch.Tensor:
+    """out = lhs @ rhs, lhs (M, K), rhs (K, N).
+
+    bf16 inputs: bf16 MFMA with fp32 accumulation, bf16 output.
+    Reference: workspaces/matmul/runs/matmul_v1.py:10-111, forward ``lhs @ rhs``.
+    """
+    _check("lhs", lhs, lhs.dtype)
+    _check("rhs", rhs, lhs.dtype)
+    _same_device(lhs, rhs)
+    m, k, n = _gemm_dims("lhs", lhs, "rhs", rhs)
+    if lhs.dtype != BF16:
+        raise ValueError(f"matmul: unsupported dtype {lhs.dtype}")
+    out = torch.empty((m, n), dtype=BF16, device=lhs.device)
+    _lib.call("kda_matmul_bf16", lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), m, k, n, _stream(lhs))
+    return out
+
+
+def rmsnorm_matmul(x: torch.Tensor, w: torch.Tensor, gamma: Optional[torch.Tensor] = None,
+                   eps: float = 0.0) -> torch.Tensor:
+    """out = (x * rsqrt(mean_k(x^2) + eps) * gamma) @ w, fused in one GEMM kernel.
+
+    x (M, K), w (K, N), gamma (K,) or None (no gain).  bf16 inputs: bf16 output,
+    fp32 accumulation and fp32 norm statistics.
+    Reference: workspaces/rmsnorm_matmul/runs/rmsnorm_matmul_v1.py:10-138
+    (forward x/sqrt(sum(x^2/K)) @ w: gamma=None, eps=0); with gain and eps as in
+    workspaces/add_rmsnorm_matmul/runs/offline_bf16_split_sim.py:97-106.
+    """
+    _check("x", x, x.dtype)
+    _check("w", w, x.dtype)
+    _same_device(x, w)
+    m, k, n = _gemm_dims("x", x, "w", w)
+    if x.dtype != BF16:
+        raise ValueError(f"rmsnorm_matmul: unsupported dtype {x.dtype}")
+    if gamma is None:
+        gamma = torch.ones(k, dtype=BF16, device=x.device)
+    _check("gamma", gamma, BF16, shape=(k,))
+    _same_device(x, gamma)
+    out = torch.empty((m, n), dtype=BF16, device=x.device)
+    _lib.call("kda_rmsnorm_matmul_bf16", x.data_ptr(), gamma.data_ptr(), w.data_ptr(),
+              out.data_ptr(), m, k, n, float(eps), _stream(x))
+    return out
+
+
+def swiglu(x: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor, w_gate: torch.Tensor,
+           h_workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out = (silu(x @ w_gate) * (x @ w_up)) @ w_down.
+
+    x (M, K), w_up/w_gate (K, F), w_down (F, K); argument order of the reference
+    forward(x, w_up, w_down, w_gate) (workspaces/swiglu/docs/draft-phase1.md:11-17,
+    kernel in workspaces/swiglu/runs/swiglu_v1.py:38-146).  bf16: the gated
+    activation h (M, F) is produced by one fused dual-GEMM kernel (gate and up
+    share each x tile; silu(gate)*up in the epilogue) and consumed by the down
+    GEMM.  ``h_workspace`` optionally supplies h's (M, F) bf16 buffer.
+    """
+    _check("x", x, x.dtype)
+    for name, t in (("w_up", w_up), ("w_down", w_down), ("w_gate", w_gate)):
+        _check(name, t, x.dtype, ndim=2)
+    _same_device(x, w_up, w_down, w_gate)
+    m, k, f = _gemm_dims("x", x, "w_up", w_up)
+    if tuple(w_gate.shape) != (k, f) or tuple(w_down.shape) != (f, k):
+        raise ValueError(f"swiglu: w_gate must be {(k, f)} and w_down {(f, k)}, got "
+                         f"{tuple(w_gate.shape)}, {tuple(w_down.shape)}")
+    if x.dtype != BF16:
+        raise ValueError(f"swiglu: unsupported dtype {x.dtype}")
+    if h_workspace is None:
+        h_workspace = torch.empty((m, f), dtype=BF16, device=x.device)
+    _check("h_workspace", h_workspace, BF16, shape=(m, f))
+    out = torch.empty((m, k), dtype=BF16, device=x.device)
+    _lib.call("kda_swiglu_bf16", x.data_ptr(), w_up.data_ptr(), w_down.data_ptr(), w_gate.data_ptr(),
+              h_workspace.data_ptr(), out.data_ptr(), m, k, f, _stream(x))
     return out
