@@ -99,6 +99,21 @@ int kda_swiglu_bf16(const kda_bf16* x, const kda_bf16* w_up, const kda_bf16* w_d
                     const kda_bf16* w_gate, kda_bf16* h, kda_bf16* y, int64_t m, int64_t k,
                     int64_t f, void* stream);
 
+/* ---------------------------------------------------------------- attention */
+
+/* Grouped-query softmax attention forward, bf16 in/out, fp32 online softmax:
+ *   out[b,s,h,:] = softmax_j(q[b,s,h,:] . k[b,j,h/G,:] * scale) @ v[b,j,h/G,:]
+ * q [B,S,Hq,D], k/v [B,S,Hkv,D] dense (BSHD); G = Hq/Hkv must be 4 and D 128.
+ * causal != 0 masks keys j > s.  The output element (b,s,h,d) is written at
+ * out + b*out_stride_b + s*out_stride_s + h*out_stride_h + d (strides in elements,
+ * multiples of 4): BSHD (S*Hq*D, Hq*D, D) or BHSD (Hq*S*D, D, S*D).
+ * Replaces kernel(v1=q, v2=k, v3=v) of
+ * workspaces/gqa_full/runs/gqa_full_v7a_exp_from_psum.py:15-220 (non-causal, BHSD out). */
+int kda_gqa_fwd_bf16(const kda_bf16* q, const kda_bf16* k, const kda_bf16* v, kda_bf16* out,
+                     int64_t batch, int64_t seq, int64_t hq, int64_t hkv, int64_t head_dim,
+                     float scale, int causal, int64_t out_stride_b, int64_t out_stride_s,
+                     int64_t out_stride_h, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -30,6 +30,8 @@ SIGNATURES = {
     "kda_matmul_bf16": [_p, _p, _p, _i64, _i64, _i64, _p],
     "kda_rmsnorm_matmul_bf16": [_p, _p, _p, _p, _i64, _i64, _i64, _f32, _p],
     "kda_swiglu_bf16": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
+    "kda_gqa_fwd_bf16": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _int,
+                         _i64, _i64, _i64, _p],
 }
 
 

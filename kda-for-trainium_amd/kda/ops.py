@@ -25,6 +25,7 @@ __all__ = [
     "matmul",
     "rmsnorm_matmul",
     "swiglu",
+    "gqa",
 ]
 
 BF16 = torch.bfloat16
@@ -221,4 +222,43 @@ def swiglu(x: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor, w_gate: to
     out = torch.empty((m, k), dtype=BF16, device=x.device)
     _lib.call("kda_swiglu_bf16", x.data_ptr(), w_up.data_ptr(), w_down.data_ptr(), w_gate.data_ptr(),
               h_workspace.data_ptr(), out.data_ptr(), m, k, f, _stream(x))
+    return out
+
+
+# ----------------------------------------------------------------- attention
+
+def gqa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False,
+        scale: Optional[float] = None, out_layout: str = "bshd") -> torch.Tensor:
+    """Grouped-query softmax attention: per query head h (kv head h // (Hq/Hkv)),
+    ``softmax(q k^T * scale) v`` with an fp32 online softmax (flash style).
+
+    q (B, S, Hq, D), k/v (B, S, Hkv, D); scale defaults to 1/sqrt(D); causal masks
+    keys after the query.  out_layout "bshd" returns (B, S, Hq, D); "bhsd" returns
+    (B, Hq, S, D), the layout of the reference's gqa_full output
+    (workspaces/gqa_full/docs/draft-phase1.md:41-43; forward in
+    workspaces/gqa_full/runs/offline_score_bf16_split_sim.py:100-123).
+    """
+    _check("q", q, q.dtype, ndim=4)
+    _check("k", k, q.dtype, ndim=4)
+    _check("v", v, q.dtype, ndim=4)
+    _same_device(q, k, v)
+    bsz, s, hq, d = q.shape
+    if tuple(k.shape) != tuple(v.shape) or k.shape[0] != bsz or k.shape[1] != s or k.shape[3] != d:
+        raise ValueError(f"gqa: k/v shape {tuple(k.shape)}/{tuple(v.shape)} incompatible with q {tuple(q.shape)}")
+    hkv = k.shape[2]
+    if hq % hkv:
+        raise ValueError(f"gqa: Hq={hq} is not a multiple of Hkv={hkv}")
+    sc = (1.0 / math.sqrt(d)) if scale is None else float(scale)
+    if q.dtype != BF16:
+        raise ValueError(f"gqa: unsupported dtype {q.dtype}")
+    if out_layout == "bshd":
+        out = torch.empty((bsz, s, hq, d), dtype=BF16, device=q.device)
+        strides = (s * hq * d, hq * d, d)
+    elif out_layout == "bhsd":
+        out = torch.empty((bsz, hq, s, d), dtype=BF16, device=q.device)
+        strides = (hq * s * d, d, s * d)
+    else:
+        raise ValueError(f"gqa: out_layout must be 'bshd' or 'bhsd', got {out_layout!r}")
+    _lib.call("kda_gqa_fwd_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+              bsz, s, hq, hkv, d, sc, 1 if causal else 0, *strides, _stream(q))
     return out

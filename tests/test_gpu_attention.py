@@ -1,0 +1,74 @@
+"""GPU parity: grouped-query flash attention (bf16, fp32 online softmax) vs the oracle.
+
+Full-size causal configuration (B4 S4096 Hq32 Hkv8 D128): the GPU computes the
+whole output; the oracle checks a sample of (batch, head) slices per seed.
+Gate: relative-L2 <= 1e-2 (bf16)."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import SEEDS, to_dev, to_host
+from kda import ops
+from oracle import inputs as oi
+from oracle import ops as oo
+from oracle.numerics import rel_l2
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+GATE = 1e-2
+
+
+def test_gqa_causal_config_full_size_sampled_heads(dev):
+    for s in SEEDS:
+        d = oi.draw("gqa_cfg", s)
+        out = ops.gqa(*(to_dev(d[k], dev, BF) for k in ("q", "k", "v")), causal=True)
+        out = to_host(out)
+        rng = np.random.default_rng(s)
+        heads = [(0, 0), (3, 31)] + [(int(rng.integers(4)), int(rng.integers(32))) for _ in range(2)]
+        want = oo.gqa(d["q"], d["k"], d["v"], causal=True, heads=heads)
+        got = np.stack([out[b, :, h, :] for b, h in heads])
+        err = rel_l2(got, want)
+        print(f"gqa_cfg seed={s} heads={heads} rel_l2={err:.3e}", flush=True)
+        assert err < GATE
+        assert np.isfinite(out).all()
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dims", [dict(B=1, S=64, HQ=4, HKV=1), dict(B=2, S=256, HQ=8, HKV=2),
+                                  dict(B=1, S=100, HQ=4, HKV=1), dict(B=1, S=1, HQ=4, HKV=1),
+                                  dict(B=2, S=333, HQ=8, HKV=2)])
+def test_gqa_small_full_compare(dev, causal, dims):
+    d = oi.draw("gqa_cfg", 7, dims=dict(dims, D=128))
+    out = to_host(ops.gqa(*(to_dev(d[k], dev, BF) for k in ("q", "k", "v")), causal=causal))
+    want = oo.gqa(d["q"], d["k"], d["v"], causal=causal)
+    err = rel_l2(out, want)
+    print(f"gqa {dims} causal={causal} rel_l2={err:.3e}", flush=True)
+    assert err < 5e-3
+
+
+def test_gqa_bhsd_layout_and_custom_scale(dev):
+    d = oi.draw("gqa_cfg", 9, dims=dict(B=1, S=192, HQ=8, HKV=2, D=128))
+    qkv = [to_dev(d[k], dev, BF) for k in ("q", "k", "v")]
+    a = to_host(ops.gqa(*qkv, causal=False, scale=0.05, out_layout="bhsd"))
+    want = oo.gqa(d["q"], d["k"], d["v"], causal=False, scale=0.05, out_layout="bhsd")
+    assert a.shape == (1, 8, 192, 128)
+    assert rel_l2(a, want) < 5e-3
+    b = to_host(ops.gqa(*qkv, causal=False, scale=0.05))
+    np.testing.assert_array_equal(a, b.transpose(0, 2, 1, 3))
+
+
+def test_gqa_causal_first_row_is_v0(dev):
+    d = oi.draw("gqa_cfg", 11, dims=dict(B=2, S=128, HQ=8, HKV=2, D=128))
+    out = to_host(ops.gqa(*(to_dev(d[k], dev, BF) for k in ("q", "k", "v")), causal=True))
+    np.testing.assert_array_equal(out[:, 0], np.repeat(d["v"][:, 0], 4, axis=1))
+
+
+def test_gqa_rejects_unsupported(dev):
+    q = torch.zeros(1, 8, 4, 64, device=dev, dtype=BF)
+    kv = torch.zeros(1, 8, 1, 64, device=dev, dtype=BF)
+    with pytest.raises(ValueError, match="head_dim"):
+        ops.gqa(q, kv, kv)
+    q = torch.zeros(1, 8, 6, 128, device=dev, dtype=BF)
+    kv = torch.zeros(1, 8, 3, 128, device=dev, dtype=BF)
+    with pytest.raises(ValueError, match="query heads per kv head"):
+        ops.gqa(q, kv, kv)
