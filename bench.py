@@ -42,10 +42,10 @@ CONFIGS = {
                  work=2048 * 8192 * 8, kernels=["silu_vec_kernel"]),
     "rmsnorm_matmul": dict(desc="RMSNorm->matmul bf16 x[4096,4096] W[4096,11008]", dtype="bf16",
                            bound="mfma", work=2 * 4096 * 4096 * 11008,
-                           kernels=["gemm_bf16_kernel<256,128,1,kRmsNorm>"]),
+                           kernels=["rms_prep_kernel", "gemm_bf16_kernel<256,256,1,kRowScale>"]),
     "swiglu": dict(desc="SwiGLU bf16 x[2048,4096] Wg/Wu[4096,14336] Wd[14336,4096]", dtype="bf16",
                    bound="mfma", work=6 * 2048 * 4096 * 14336,
-                   kernels=["gemm_bf16_kernel<256,64,2,kSwiGLU>", "gemm_bf16_kernel<256,128,1,kPlain>"]),
+                   kernels=["gemm_bf16_kernel<256,128,2,kSwiGLU>", "gemm_bf16_kernel<256,128,1,kStore>"]),
     "adamw": dict(desc="AdamW fp32 n=2^27 in-place step 10", dtype="fp32", bound="hbm",
                   work=28 * (1 << 27), kernels=["adamw_vec_kernel<true>"]),
     "gqa": dict(desc="causal GQA bf16 B4 S4096 Hq32 Hkv8 D128", dtype="bf16", bound="mfma",

@@ -82,14 +82,20 @@ int kda_rope_f32(const float* x, const float* cos_t, const float* sin_t, float* 
 int kda_matmul_bf16(const kda_bf16* a, const kda_bf16* b, kda_bf16* c, int64_t m, int64_t k,
                     int64_t n, void* stream);
 
-/* y[M,N] = (x * rsqrt(mean_k(x^2) + eps) * gamma) @ w, x [M,K], gamma [K] (8-byte
- * aligned), w [K,N].  RMSNorm fused into the GEMM: one kernel, x read once per tile.
+/* y[M,N] = (x * rsqrt(mean_k(x^2) + eps) * gamma) @ w, x [M,K], gamma [K] (16-byte
+ * aligned), w [K,N].  A streaming pre-pass reads x once and writes the per-row
+ * 1/rms (fp32) and bf16(x * gamma) into `workspace`; the GEMM applies 1/rms to
+ * its accumulators in the epilogue.  `workspace` is caller-owned device memory
+ * of at least kda_rmsnorm_matmul_bf16_workspace_size(m, k) bytes, 16-byte aligned.
  * Replaces kernel(v1=x, v2=w) of workspaces/rmsnorm_matmul/runs/rmsnorm_matmul_v1.py:10-138
  * (which has no gain and no eps) and the x+z-free part of
  * workspaces/add_rmsnorm_matmul/runs/add_rmsnorm_matmul_v1.py:8-146 (gain g, eps). */
 int kda_rmsnorm_matmul_bf16(const kda_bf16* x, const kda_bf16* gamma, const kda_bf16* w,
                             kda_bf16* y, int64_t m, int64_t k, int64_t n, float eps,
-                            void* stream);
+                            void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Bytes of workspace kda_rmsnorm_matmul_bf16 needs for an [m, k] x (-1 if negative). */
+int64_t kda_rmsnorm_matmul_bf16_workspace_size(int64_t m, int64_t k);
 
 /* y[M,K] = (silu(x @ w_gate) * (x @ w_up)) @ w_down with x [M,K], w_up/w_gate [K,F],
  * w_down [F,K].  h is caller-provided scratch of M*F bf16 (the gated activation,

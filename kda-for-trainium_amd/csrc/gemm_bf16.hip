@@ -1,65 +1,79 @@
 // bf16 GEMM family on gfx950 MFMA (v_mfma_f32_16x16x32_bf16), fp32 accumulation.
 //
-//   C[M,N] = A[M,K] @ B[K,N]        A, B, C row-major bf16
+//   C[M,N] = A[M,K] @ B[K,N]      bf16 operands, bf16 (or fp32) output
 //
-// Variants (template `Mode`):
-//   kPlain    C = A @ B
-//   kRmsNorm  C = (A * rsqrt(mean_k(A^2) + eps) * gamma) @ B.  The per-row sum of
-//             squares is accumulated from the A tiles as they stream through the
-//             workgroup (every workgroup sees its rows' full K), gamma scales the
-//             rows of each B tile while it is staged into LDS, and the per-row
-//             rsqrt is applied to the fp32 accumulators in the epilogue.  One
-//             kernel, no extra HBM traffic.
-//   kSwiGLU   H = silu(A @ Bg) * (A @ Bu): two B operands share each A tile; the
-//             epilogue applies silu(gate) * up and stores H.
+// Data path (per workgroup = one BM x BN output tile, 4 waves in a 2 x 2 grid,
+// each wave owning a (BM/2) x (BN/2) accumulator block in AGPR/VGPR):
 //
-// Tiling: one 256-thread workgroup (4 waves, 2x2) per BM x BN output tile; each
-// wave owns a (BM/2) x (BN/2) sub-tile held in MFMA accumulators.  K advances in
-// BK=64 steps through a double-buffered LDS ring: while the MFMAs consume stage
-// s, the next K-step is already in flight from HBM into registers and is
-// written to stage s^1 afterwards (one barrier per K-step).
+//   HBM --global_load_lds_dwordx4--> LDS (2-stage ring, BK = 64) --ds_read--> MFMA
 //
-// LDS layout: both operands are stored K-contiguous ([row][64] bf16, 128 B per
-// row) so one ds_read_b128 yields an MFMA fragment (8 consecutive k).  The 16 B
-// chunk index within a row is XOR-swizzled with (row & 7), which makes the
-// fragment reads (8 consecutive rows, same chunk) and the staging writes hit
-// distinct banks.  A is copied as-is; B arrives N-contiguous from HBM and is
-// transposed in registers (4 k-rows x 8 n per thread, v_perm_b32 or, with the
-// gamma scale, v_cvt_pk_bf16_f32) before its LDS write.
+//   * Operands go straight from global memory into LDS (16 bytes per lane, no
+//     register staging, no VALU work): each wave instruction fills 1 KiB of
+//     LDS lane-linearly, so the LDS swizzle is applied on the global side by
+//     choosing which 16-byte chunk each lane fetches.
+//   * K-contiguous operands (A row-major) are stored [rows][64 k], 128 B rows,
+//     16-byte chunk c of row r at position c ^ kswz(r); one ds_read_b128 gives
+//     an MFMA fragment (one row, 8 consecutive k).
+//   * MN-contiguous operands (B row-major [K][N], or A stored [K][M]) are kept in
+//     their HBM orientation: [64 k][cols], 32-byte segment s of row k at
+//     position s ^ mswz(k).  The fragment (one column, 8 consecutive k) is read
+//     with two ds_read_b64_tr_b16: within each 16-lane group, lane 4r+q names
+//     4 elements of k-row r and lane j receives column j of that 4 x 16 block,
+//     i.e. the transpose happens in the LDS read.
+//   * Both swizzles keep the fragment reads free of bank conflicts for 16 (or
+//     32) lanes serviced together.
+//   * Pipeline: the DMA of k-tile kt+1 is issued right after the barrier that
+//     publishes k-tile kt, so it overlaps the 2 x TM x TN MFMAs of tile kt.
+//     One s_waitcnt vmcnt(0) + s_barrier per k-tile; no fences.
 //
-// MFMA operand order: the B fragment is passed as the MFMA "A" operand and the
-// A fragment as "B", so each lane's 4 accumulators are 4 consecutive columns of
-// one output row -> one 8-byte store per lane per 16x16 sub-tile.
+// MFMA operand order: the B fragment is the MFMA "A" operand and the A fragment
+// the "B" operand, so each lane's 4 accumulators are 4 consecutive columns of
+// one output row (8-byte bf16 stores).
 //
-// Workgroup -> tile mapping: workgroups are dealt round-robin to the 8 XCDs, so
-// consecutive tile ids are remapped to land on the same XCD (sharing its L2),
-// then ordered in groups of kGroupM tile-rows so concurrently running tiles
-// reuse the same A rows and B columns.
+// Tile order: workgroups are dealt round-robin to the 8 XCDs, so consecutive
+// tile ids are remapped onto one XCD (sharing its L2), then walked in groups of
+// kGroupM tile-rows so co-resident tiles reuse the same A rows and B columns.
+//
+// Epilogues: plain store; per-row scale (the RMSNorm 1/rms, whose statistics
+// and gamma-scaled bf16 copy of x come from a streaming pre-pass over x, see
+// rms_prep_kernel); SwiGLU (two B operands, silu(gate) * up); fp32 store.
 #include "common.h"
 
 namespace kda {
 namespace gemm {
 
-enum class Mode { kPlain, kRmsNorm, kSwiGLU };
-
 constexpr int kThreads = 256;
-constexpr int BK = 64;        // K per stage (bf16 elements)
-constexpr int kGroupM = 8;    // tile-rows per scheduling group
+constexpr int BK = 64;
+constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
 
-struct Args {
-  const uint16_t* a;      // [M][K]
-  const uint16_t* b;      // [K][N]  (gate weights for SwiGLU)
-  const uint16_t* b2;     // [K][N]  up weights (SwiGLU only)
-  const uint16_t* gamma;  // [K]     (RmsNorm only)
-  uint16_t* c;            // [M][N]
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+#define KDA_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+// 16 zero bytes: the DMA source for k-chunks past K (so they contribute 0).
+__device__ __align__(16) uint32_t g_zero_chunk[4] = {0u, 0u, 0u, 0u};
+
+enum class Epi { kStore, kRowScale, kSwiGLU, kStoreF32 };
+
+struct Params {
+  const uint16_t* a;   // A_KMAJ: a[m*lda + k]; else a[k*lda + m]
+  const uint16_t* b;   // b[k*ldb + n]            (gate weights for SwiGLU)
+  const uint16_t* b2;  // b2[k*ldb + n]           (up weights, SwiGLU only)
+  void* c;             // c[m*ldc + n]  (bf16, or fp32 for kStoreF32)
+  const float* row_scale;  // [M] (kRowScale)
+  int64_t lda, ldb, ldc;
+  int64_t batch_a, batch_b, batch_c;   // per-batch strides (elements), batch = blockIdx.y
   int m, n, k;
-  float eps;
 };
 
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ (row & 7); }
+// Position of 16-byte chunk c of row r in a K-contiguous tile (128-byte rows).
+__device__ __forceinline__ int kswz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+// Position of 32-byte segment s of k-row k in an MN-contiguous tile.
+__device__ __forceinline__ int mswz(int k) { return (k & 3) | (((k >> 3) & 1) << 2); }
 
-// Maps a linear workgroup id to (tile_m, tile_n): XCD-contiguous, grouped by rows.
+// Maps the linear workgroup id to (tile_m, tile_n): XCD-contiguous, grouped by rows.
 __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
   const int total = tiles_m * tiles_n;
   int pid = blockIdx.x;
@@ -76,142 +90,157 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, i
 
 __device__ __forceinline__ float silu_f(float x) { return __fdividef(x, 1.0f + __expf(-x)); }
 
-template <int BM, int BN, int NB, Mode MODE, bool CHECK>
-__global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(Args p) {
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2{lo, hi}), bf16x2));
+}
+
+// One 16-byte-per-lane DMA from global memory into LDS: lane i's 16 bytes at
+// `sbase + voff` land at LDS byte `lds + 16*i`.  Issued as inline asm so the
+// compiler does not treat it as an LDS store (it would otherwise wait for it
+// with vmcnt(0) before every later LDS read, which serialises the prefetch);
+// completion is awaited explicitly (s_waitcnt vmcnt) before the barrier that
+// publishes the stage.  The leading s_nop covers the M0-write hazard.
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds)
+               : "memory");
+}
+// Same with a per-lane 64-bit address (used for the K tail, where lanes past K
+// read a zero chunk).
+__device__ __forceinline__ void dma16_ptr(const void* src, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)KDA_LDS_PTR(p);
+}
+
+// Reads the MFMA fragment (column `col`, k = kbase + 8*(lane/16) .. +7) of an
+// MN-contiguous [64][COLS] tile; `col0` is the first column of the 16-column block.
+template <int COLS>
+__device__ __forceinline__ bf16x8 read_mn_frag(const uint8_t* tile, int col0, int kbase, int lane) {
+  const int g = lane >> 4, jj = lane & 15;
+  const int s = col0 >> 4;
+  const int k0 = kbase + 8 * g + (jj >> 2);
+  const int k1 = k0 + 4;
+  const uint8_t* p0 = tile + k0 * (2 * COLS) + ((s ^ mswz(k0)) << 5) + 8 * (jj & 3);
+  const uint8_t* p1 = tile + k1 * (2 * COLS) + ((s ^ mswz(k1)) << 5) + 8 * (jj & 3);
+  const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16*)KDA_LDS_PTR(p0));
+  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16*)KDA_LDS_PTR(p1));
+  typedef short v8i16 __attribute__((ext_vector_type(8)));
+  const v8i16 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// Reads the MFMA fragment (row `row`, k = kbase + 8*(lane/16) .. +7) of a
+// K-contiguous [ROWS][64] tile.
+__device__ __forceinline__ bf16x8 read_k_frag(const uint8_t* tile, int row, int kbase, int lane) {
+  const int c = (kbase >> 3) + (lane >> 4);
+  return *reinterpret_cast<const bf16x8*>(tile + row * 128 + ((c ^ kswz(row)) << 4));
+}
+
+template <int BM, int BN, int NB, bool A_KMAJ, Epi EPI, bool KTAIL>
+__global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(Params p) {
   static_assert(NB == 1 || NB == 2, "one or two B operands");
-  static_assert(BM % 32 == 0 && BN % 32 == 0, "tile");
-  constexpr int WM = BM / 2, WN = BN / 2;          // wave tile
-  constexpr int TM = WM / 16, TN = WN / 16;        // 16x16 sub-tiles per wave
-  constexpr int A_PASSES = BM / 32;                // 16B A chunks per thread per stage
-  constexpr int B_UNITS = NB * 2 * BN / kThreads;  // (4k x 8n) B units per thread
-  static_assert(B_UNITS >= 1 && (NB * 2 * BN) % kThreads == 0, "B unit split");
-  constexpr int A_STAGE = BM * BK;                 // bf16 elements
-  constexpr int B_STAGE = BN * BK;
+  static_assert(BM % 128 == 0 && BN % 128 == 0, "tile");
+  constexpr int WM = BM / 2, WN = BN / 2;     // wave tile (per B operand)
+  constexpr int TM = WM / 16, TN = WN / 16;   // 16x16 MFMA tiles per wave
+  constexpr int A_BYTES = BM * BK * 2;
+  constexpr int B_BYTES = BN * BK * 2;        // per B operand
+  constexpr int STAGE = A_BYTES + NB * B_BYTES;
+  constexpr int A_INST = A_BYTES / 1024 / 4;  // DMA instructions per wave per stage
+  constexpr int B_INST = B_BYTES / 1024 / 4;  // ... per B operand
+  constexpr int A_RPI = A_KMAJ ? 8 : 1024 / (2 * BM);  // tile rows per DMA instruction
+  constexpr int B_RPI = 1024 / (2 * BN);
+  constexpr int A_LPR = A_KMAJ ? 8 : 2 * BM / 16;       // lanes per tile row
+  constexpr int B_LPR = 2 * BN / 16;
 
-  extern __shared__ __align__(16) uint16_t smem[];
-  uint16_t* As = smem;                             // [2][BM][BK]
-  uint16_t* Bs = smem + 2 * A_STAGE;               // [2][NB][BN][BK]
-  __shared__ float s_inv_rms[MODE == Mode::kRmsNorm ? BM : 1];
+  extern __shared__ __align__(1024) uint8_t smem[];
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
   const int tiles_m = (p.m + BM - 1) / BM, tiles_n = (p.n + BN - 1) / BN;
   int tm, tn;
   tile_coords(tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int K = p.k, N = p.n, M = p.m;
-  const int ktiles = (K + BK - 1) / BK;
+  const int M = p.m, N = p.n, K = p.k;
+  const int nk = (K + BK - 1) / BK;
+  const int64_t bz = blockIdx.y;
 
-  // ---- per-thread staging assignment
-  const int a_chunk = tid & 7;           // 16B chunk (8 k) within the BK row
-  const int a_row0 = tid >> 3;           // + 32 * pass
-  u32x4 a_reg[A_PASSES];
-  u32x4 b_reg[B_UNITS][4];
-  float ssq[MODE == Mode::kRmsNorm ? A_PASSES : 1];
-  if constexpr (MODE == Mode::kRmsNorm) {
+  // ---- DMA sources.  Lane offsets are 32-bit byte offsets from the operand's
+  // (per-batch) base, which advances by a scalar amount per k-tile.  Rows/columns
+  // past M/N are clamped to the last valid one (their outputs are never stored).
+  const uint8_t* A = reinterpret_cast<const uint8_t*>(p.a + bz * p.batch_a);
+  const uint8_t* Bop[NB];
+  Bop[0] = reinterpret_cast<const uint8_t*>(p.b + bz * p.batch_b);
+  if constexpr (NB == 2) Bop[NB - 1] = reinterpret_cast<const uint8_t*>(p.b2 + bz * p.batch_b);
+  uint32_t a_off[A_INST];
+  int a_k[A_INST];   // k (within the k-tile) of the lane's data, for the K tail
 #pragma unroll
-    for (int i = 0; i < A_PASSES; ++i) ssq[i] = 0.f;
+  for (int j = 0; j < A_INST; ++j) {
+    const int q = j * 4 + wave;
+    const int r = q * A_RPI + lane / A_LPR;
+    const int t = lane % A_LPR;
+    if constexpr (A_KMAJ) {
+      const int c = t ^ kswz(r);
+      const int gm = min(m0 + r, M - 1);
+      a_off[j] = (uint32_t)(((int64_t)gm * p.lda + 8 * c) * 2);
+      a_k[j] = 8 * c;
+    } else {
+      const int s = (t >> 1) ^ mswz(r);
+      const int gm = min(m0 + s * 16 + (t & 1) * 8, M - 8);
+      a_off[j] = (uint32_t)(((int64_t)r * p.lda + gm) * 2);
+      a_k[j] = r;
+    }
   }
+  uint32_t b_off[B_INST];
+  int b_k[B_INST];
+#pragma unroll
+  for (int j = 0; j < B_INST; ++j) {
+    const int q = j * 4 + wave;
+    const int r = q * B_RPI + lane / B_LPR;
+    const int t = lane % B_LPR;
+    const int s = (t >> 1) ^ mswz(r);
+    const int gn = min(n0 + s * 16 + (t & 1) * 8, N - 8);
+    b_off[j] = (uint32_t)(((int64_t)r * p.ldb + gn) * 2);
+    b_k[j] = r;
+  }
+  const int64_t a_step = (A_KMAJ ? BK : BK * p.lda) * 2;   // bytes per k-tile
+  const int64_t b_step = BK * p.ldb * 2;
+  const uint32_t lds0 = lds_addr(smem);
 
-  auto load_a = [&](int kt) {
-    const int kk = kt * BK + a_chunk * 8;
+  auto issue = [&](int kt, int stage) {
+    const uint32_t base = lds0 + stage * STAGE;
+    const uint8_t* sa = A + kt * a_step;
+    const bool tail = KTAIL && (kt + 1) * BK > K;
+    if (!tail) {
 #pragma unroll
-    for (int i = 0; i < A_PASSES; ++i) {
-      const int row = a_row0 + 32 * i;
-      const int gm = m0 + row;
-      if (!CHECK || (gm < M && kk < K)) {
-        a_reg[i] = *reinterpret_cast<const u32x4*>(p.a + (size_t)gm * K + kk);
-      } else {
-        a_reg[i] = u32x4{0u, 0u, 0u, 0u};
+      for (int j = 0; j < A_INST; ++j) dma16(sa, a_off[j], base + (j * 4 + wave) * 1024);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const uint8_t* sb = Bop[b] + kt * b_step;
+#pragma unroll
+        for (int j = 0; j < B_INST; ++j)
+          dma16(sb, b_off[j], base + A_BYTES + b * B_BYTES + (j * 4 + wave) * 1024);
       }
-    }
-  };
-  auto load_b = [&](int kt) {
+    } else {
+      const int kbase = kt * BK;
 #pragma unroll
-    for (int u = 0; u < B_UNITS; ++u) {
-      const int unit = tid + u * kThreads;
-      const int which = unit / (2 * BN);
-      const int kq = unit & 15;
-      const int nc = (unit % (2 * BN)) >> 4;
-      const uint16_t* src = (NB == 2 && which) ? p.b2 : p.b;
-      const int gn = n0 + nc * 8;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int gk = kt * BK + kq * 4 + r;
-        if (!CHECK || (gk < K && gn < N)) {
-          b_reg[u][r] = *reinterpret_cast<const u32x4*>(src + (size_t)gk * N + gn);
-        } else {
-          b_reg[u][r] = u32x4{0u, 0u, 0u, 0u};
-        }
-      }
-    }
-  };
-
-  auto store_a = [&](int stage) {
-    uint16_t* dst = As + stage * A_STAGE;
-#pragma unroll
-    for (int i = 0; i < A_PASSES; ++i) {
-      const int row = a_row0 + 32 * i;
-      if constexpr (MODE == Mode::kRmsNorm) {
-        // fp32 sum of squares of the 8 bf16 values (exact widening + FMA).
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const float lo = __builtin_bit_cast(float, a_reg[i][w] << 16);
-          const float hi = __builtin_bit_cast(float, a_reg[i][w] & 0xffff0000u);
-          ssq[i] = fmaf(lo, lo, ssq[i]);
-          ssq[i] = fmaf(hi, hi, ssq[i]);
-        }
-      }
-      *reinterpret_cast<u32x4*>(dst + row * BK + swz(row, a_chunk) * 8) = a_reg[i];
-    }
-  };
-
-  auto store_b = [&](int stage, int kt) {
-#pragma unroll
-    for (int u = 0; u < B_UNITS; ++u) {
-      const int unit = tid + u * kThreads;
-      const int which = unit / (2 * BN);
-      const int kq = unit & 15;
-      const int nc = (unit % (2 * BN)) >> 4;
-      uint16_t* dst = Bs + (stage * NB + which) * B_STAGE;
-      float g[4];
-      if constexpr (MODE == Mode::kRmsNorm) {
-        const int gk = kt * BK + kq * 4;
-        if (!CHECK || gk < K) {
-          const u32x2 gb = *reinterpret_cast<const u32x2*>(p.gamma + gk);
-          g[0] = __builtin_bit_cast(float, gb[0] << 16);
-          g[1] = __builtin_bit_cast(float, gb[0] & 0xffff0000u);
-          g[2] = __builtin_bit_cast(float, gb[1] << 16);
-          g[3] = __builtin_bit_cast(float, gb[1] & 0xffff0000u);
-        } else {
-          g[0] = g[1] = g[2] = g[3] = 0.f;
-        }
+      for (int j = 0; j < A_INST; ++j) {
+        const void* src = (kbase + a_k[j] < K) ? (const void*)(sa + a_off[j]) : (const void*)g_zero_chunk;
+        dma16_ptr(src, base + (j * 4 + wave) * 1024);
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int n = nc * 8 + j;
-        const int w = j >> 1;
-        u32x2 out;
-        if constexpr (MODE == Mode::kRmsNorm) {
-          float f[4];
+      for (int b = 0; b < NB; ++b) {
+        const uint8_t* sb = Bop[b] + kt * b_step;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const uint32_t bits = (j & 1) ? (b_reg[u][r][w] & 0xffff0000u) : (b_reg[u][r][w] << 16);
-            f[r] = __builtin_bit_cast(float, bits) * g[r];
-          }
-          typedef float floatx2 __attribute__((ext_vector_type(2)));
-          typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-          out[0] = __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2{f[0], f[1]}), bf16x2));
-          out[1] = __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2{f[2], f[3]}), bf16x2));
-        } else {
-          const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-          out[0] = __builtin_amdgcn_perm(b_reg[u][1][w], b_reg[u][0][w], sel);
-          out[1] = __builtin_amdgcn_perm(b_reg[u][3][w], b_reg[u][2][w], sel);
+        for (int j = 0; j < B_INST; ++j) {
+          const void* src = (kbase + b_k[j] < K) ? (const void*)(sb + b_off[j]) : (const void*)g_zero_chunk;
+          dma16_ptr(src, base + A_BYTES + b * B_BYTES + (j * 4 + wave) * 1024);
         }
-        *reinterpret_cast<u32x2*>(dst + n * BK + swz(n, kq >> 1) * 8 + (kq & 1) * 4) = out;
       }
     }
   };
@@ -224,126 +253,211 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(Args p) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) acc[b][i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // ---- prologue: stage 0
-  load_a(0);
-  load_b(0);
-  store_a(0);
-  store_b(0, 0);
-  __syncthreads();
+  // Fragment readers for one 32-wide k half (kh) of the current stage.
+  auto read_a = [&](const uint8_t* at, int kh, int i) -> bf16x8 {
+    if constexpr (A_KMAJ)
+      return read_k_frag(at, wm * WM + i * 16 + (lane & 15), kh * 32, lane);
+    else
+      return read_mn_frag<BM>(at, wm * WM + i * 16, kh * 32, lane);
+  };
+  auto read_b = [&](const uint8_t* bt, int kh, int bj) -> bf16x8 {
+    const int b = bj / TN, j = bj % TN;
+    return read_mn_frag<BN>(bt + b * B_BYTES, wn * WN + j * 16, kh * 32, lane);
+  };
+  constexpr int KH = BK / 32;               // k halves per stage
+  constexpr int NBF = NB * TN;              // B fragments per k half
+  static_assert(NBF % TM == 0 || TM % NBF == 0, "B prefetch split");
+  constexpr int B_PER_GROUP = (NBF + TM - 1) / TM;
 
-  const int frag_row = lane & 15;
-  const int frag_chunk = lane >> 4;   // 0..3 within a 32-k half
-
-  for (int kt = 0; kt < ktiles; ++kt) {
+  issue(0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
     const int stage = kt & 1;
-    const bool more = kt + 1 < ktiles;
-    if (more) {
-      load_a(kt + 1);
-      load_b(kt + 1);
-    }
-    const uint16_t* as = As + stage * A_STAGE;
-    const uint16_t* bs = Bs + stage * NB * B_STAGE;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (kt + 1 < nk) issue(kt + 1, stage ^ 1);
+    const uint8_t* at = smem + stage * STAGE;
+    const uint8_t* bt = at + A_BYTES;
+    // Software pipeline over MFMA groups g = (kh, i): group g multiplies A
+    // fragment i against the NB*TN B fragments of half kh, while the A fragment
+    // of group g+1 and a slice of the next half's B fragments are in flight.
+    bf16x8 af[2], bfr[2][NBF];
 #pragma unroll
-    for (int kh = 0; kh < BK / 32; ++kh) {
-      const int chunk = kh * 4 + frag_chunk;
-      bf16x8 af[TM];
-      bf16x8 bfr[NB][TN];
+    for (int bj = 0; bj < NBF; ++bj) bfr[0][bj] = read_b(bt, 0, bj);
+    af[0] = read_a(at, 0, 0);
+#pragma unroll
+    for (int kh = 0; kh < KH; ++kh) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
-        const int row = wm * WM + i * 16 + frag_row;
-        af[i] = *reinterpret_cast<const bf16x8*>(as + row * BK + swz(row, chunk) * 8);
-      }
+        const int g = kh * TM + i;
+        if (i + 1 < TM)
+          af[(g + 1) & 1] = read_a(at, kh, i + 1);
+        else if (kh + 1 < KH)
+          af[(g + 1) & 1] = read_a(at, kh + 1, 0);
+        if (kh + 1 < KH) {
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const int row = wn * WN + j * 16 + frag_row;
-          bfr[b][j] = *reinterpret_cast<const bf16x8*>(bs + b * B_STAGE + row * BK + swz(row, chunk) * 8);
+          for (int u = 0; u < B_PER_GROUP; ++u) {
+            const int bj = i * B_PER_GROUP + u;
+            if (bj < NBF) bfr[(kh + 1) & 1][bj] = read_b(bt, kh + 1, bj);
+          }
         }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int b = 0; b < NB; ++b)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
-            acc[b][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[b][j], af[i], acc[b][i][j], 0, 0, 0);
+            acc[b][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[kh & 1][b * TN + j], af[g & 1],
+                                                                   acc[b][i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    if (more) {
-      store_a(stage ^ 1);
-      store_b(stage ^ 1, kt + 1);
-    }
-    __syncthreads();
   }
 
-  // ---- RMSNorm: reduce the per-row sums of squares (8 lanes share a row)
-  if constexpr (MODE == Mode::kRmsNorm) {
-    const float inv_k = 1.0f / (float)K;
-#pragma unroll
-    for (int i = 0; i < A_PASSES; ++i) {
-      float s = ssq[i];
-      s += __shfl_xor(s, 1);
-      s += __shfl_xor(s, 2);
-      s += __shfl_xor(s, 4);
-      if (a_chunk == 0) s_inv_rms[a_row0 + 32 * i] = 1.0f / sqrtf(s * inv_k + p.eps);
-    }
-    __syncthreads();
-  }
-
-  // ---- epilogue: lane holds C[row][col..col+3]
+  // ---- epilogue: lane holds C[row][col .. col+3] for each 16x16 tile
   const int col_in = (lane >> 4) * 4;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
-    const int row = wm * WM + i * 16 + frag_row;
-    const int gm = m0 + row;
+    const int gm = m0 + wm * WM + i * 16 + (lane & 15);
+    if (gm >= M) continue;
     float scale = 1.0f;
-    if constexpr (MODE == Mode::kRmsNorm) scale = s_inv_rms[row];
+    if constexpr (EPI == Epi::kRowScale) scale = p.row_scale[gm];
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int gn = n0 + wn * WN + j * 16 + col_in;
-      if (CHECK && (gm >= M || gn >= N)) continue;
+      if (gn >= N) continue;
       float v[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        if constexpr (MODE == Mode::kSwiGLU) {
+        if constexpr (EPI == Epi::kSwiGLU)
           v[r] = silu_f(acc[0][i][j][r]) * acc[NB - 1][i][j][r];
-        } else {
+        else
           v[r] = acc[0][i][j][r] * scale;
-        }
       }
-      typedef float floatx2 __attribute__((ext_vector_type(2)));
-      typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-      u32x2 o;
-      o[0] = __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2{v[0], v[1]}), bf16x2));
-      o[1] = __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2{v[2], v[3]}), bf16x2));
-      *reinterpret_cast<u32x2*>(p.c + (size_t)gm * N + gn) = o;
+      const int64_t off = bz * p.batch_c + (int64_t)gm * p.ldc + gn;
+      if constexpr (EPI == Epi::kStoreF32) {
+        *reinterpret_cast<floatx4*>(reinterpret_cast<float*>(p.c) + off) =
+            floatx4{v[0], v[1], v[2], v[3]};
+      } else {
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.c) + off) =
+            u32x2{pack2(v[0], v[1]), pack2(v[2], v[3])};
+      }
     }
   }
 }
 
-template <int BM, int BN, int NB, Mode MODE>
-int launch(const Args& a, hipStream_t st, const char* what) {
+// ---------------------------------------------------------------- RMSNorm pre-pass
+// One workgroup per row: inv_rms[m] = 1/sqrt(mean_k x[m,k]^2 + eps) (fp32 sum of
+// squares of the bf16 values) and xg[m,k] = bf16(x[m,k] * gamma[k]).  x is read
+// once; xg stays in the 256 MB Infinity Cache for the GEMM that follows.
+constexpr int kPrepThreads = 256;
+constexpr int kPrepVec = 4;   // 16-byte chunks per thread held in registers (K <= 8192)
+
+__global__ __launch_bounds__(kPrepThreads) void rms_prep_kernel(const uint16_t* __restrict__ x,
+                                                                const uint16_t* __restrict__ gamma,
+                                                                uint16_t* __restrict__ xg,
+                                                                float* __restrict__ inv_rms, int k,
+                                                                float eps) {
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nchunk = k / 8;
+  const u32x4* xr = reinterpret_cast<const u32x4*>(x + (int64_t)row * k);
+  u32x4 v[kPrepVec];
+  float ssq = 0.f;
+#pragma unroll
+  for (int u = 0; u < kPrepVec; ++u) {
+    const int c = tid + u * kPrepThreads;
+    v[u] = (c < nchunk) ? __builtin_nontemporal_load(xr + c) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float lo = __builtin_bit_cast(float, v[u][w] << 16);
+      const float hi = __builtin_bit_cast(float, v[u][w] & 0xffff0000u);
+      ssq = fmaf(lo, lo, ssq);
+      ssq = fmaf(hi, hi, ssq);
+    }
+  }
+  // tail chunks beyond the register-held part (K > 8192)
+  for (int c = tid + kPrepVec * kPrepThreads; c < nchunk; c += kPrepThreads) {
+    const u32x4 t = xr[c];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float lo = __builtin_bit_cast(float, t[w] << 16);
+      const float hi = __builtin_bit_cast(float, t[w] & 0xffff0000u);
+      ssq = fmaf(lo, lo, ssq);
+      ssq = fmaf(hi, hi, ssq);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ssq += __shfl_xor(ssq, off);
+  __shared__ float part[kPrepThreads / 64];
+  __shared__ float s_inv;
+  if ((tid & 63) == 0) part[tid >> 6] = ssq;
+  __syncthreads();
+  if (tid == 0) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < kPrepThreads / 64; ++w) s += part[w];
+    const float inv = 1.0f / sqrtf(s / (float)k + eps);
+    s_inv = inv;
+    inv_rms[row] = inv;
+  }
+  __syncthreads();
+  (void)s_inv;
+  const u32x4* gr = reinterpret_cast<const u32x4*>(gamma);
+  u32x4* outr = reinterpret_cast<u32x4*>(xg + (int64_t)row * k);
+  auto scale_store = [&](const u32x4& t, int c) {
+    const u32x4 g = gr[c];
+    u32x4 o;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float x0 = __builtin_bit_cast(float, t[w] << 16);
+      const float x1 = __builtin_bit_cast(float, t[w] & 0xffff0000u);
+      const float g0 = __builtin_bit_cast(float, g[w] << 16);
+      const float g1 = __builtin_bit_cast(float, g[w] & 0xffff0000u);
+      o[w] = pack2(x0 * g0, x1 * g1);
+    }
+    outr[c] = o;
+  };
+#pragma unroll
+  for (int u = 0; u < kPrepVec; ++u) {
+    const int c = tid + u * kPrepThreads;
+    if (c < nchunk) scale_store(v[u], c);
+  }
+  for (int c = tid + kPrepVec * kPrepThreads; c < nchunk; c += kPrepThreads) scale_store(xr[c], c);
+}
+
+// ---------------------------------------------------------------- launch helpers
+
+template <int BM, int BN, int NB, bool A_KMAJ, Epi EPI>
+int launch(const Params& a, int batch, hipStream_t st, const char* what) {
   const int tiles = ((a.m + BM - 1) / BM) * ((a.n + BN - 1) / BN);
   const size_t lds = (size_t)2 * (BM + NB * BN) * BK * sizeof(uint16_t);
-  const bool full = (a.m % BM == 0) && (a.n % BN == 0) && (a.k % BK == 0);
-  // Opt in to > 64 KiB of dynamic LDS once per instantiation (process-wide;
-  // the attribute is per function, not per device).
   static const bool attr_ok = [&] {
     const hipError_t e1 = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(gemm_bf16_kernel<BM, BN, NB, MODE, false>),
+        reinterpret_cast<const void*>(gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, false>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     const hipError_t e2 = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(gemm_bf16_kernel<BM, BN, NB, MODE, true>),
+        reinterpret_cast<const void*>(gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, true>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     return e1 == hipSuccess && e2 == hipSuccess;
   }();
   if (!attr_ok) return set_error(KDA_ERR_HIP, "%s: cannot reserve %zu bytes of LDS", what, lds);
-  if (full)
-    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, NB, MODE, false>), dim3(tiles), dim3(kThreads),
+  const dim3 grid(tiles, batch);
+  if (a.k % BK == 0)
+    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, false>), grid, dim3(kThreads),
                        lds, st, a);
   else
-    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, NB, MODE, true>), dim3(tiles), dim3(kThreads),
+    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, true>), grid, dim3(kThreads),
                        lds, st, a);
   return check_launch(what);
+}
+
+// Chooses the N tile: 256 when that still gives at least one wave of tiles over
+// the device, else 128 (more, smaller tiles for skinny problems).
+template <bool A_KMAJ, Epi EPI>
+int launch_auto(const Params& a, int batch, hipStream_t st, const char* what) {
+  const int64_t tiles256 = (int64_t)((a.m + 255) / 256) * ((a.n + 255) / 256) * batch;
+  if (tiles256 >= device_cu_count()) return launch<256, 256, 1, A_KMAJ, EPI>(a, batch, st, what);
+  return launch<256, 128, 1, A_KMAJ, EPI>(a, batch, st, what);
 }
 
 int validate(const char* what, const void* a, const void* b, const void* c, int64_t m,
@@ -351,8 +465,11 @@ int validate(const char* what, const void* a, const void* b, const void* c, int6
   if (m < 0 || n < 0 || k < 0)
     return set_error(KDA_ERR_INVALID_ARG, "%s: negative size (M=%lld N=%lld K=%lld)", what,
                      (long long)m, (long long)n, (long long)k);
-  if (m > (1 << 30) || n > (1 << 30) || k > (1 << 30) || (m * k) > (int64_t(1) << 40))
+  if (m > (1 << 30) || n > (1 << 30) || k > (1 << 30))
     return set_error(KDA_ERR_UNSUPPORTED, "%s: size too large", what);
+  // 32-bit byte offsets address each operand (per batch) from a scalar base.
+  if (m * k * 2 > (int64_t)0xffffffff || k * n * 2 > (int64_t)0xffffffff)
+    return set_error(KDA_ERR_UNSUPPORTED, "%s: an operand exceeds 4 GiB", what);
   if ((k % 8) || (n % 8))
     return set_error(KDA_ERR_UNSUPPORTED,
                      "%s: K (%lld) and N (%lld) must be multiples of 8 (16-byte rows)", what,
@@ -374,22 +491,47 @@ extern "C" int kda_matmul_bf16(const kda_bf16* a, const kda_bf16* b, kda_bf16* c
   clear_error();
   if (int rc = validate("matmul_bf16", a, b, c, m, n, k)) return rc;
   if (m == 0 || n == 0) return KDA_OK;
-  Args p{a, b, nullptr, nullptr, c, (int)m, (int)n, (int)k, 0.f};
-  return launch<256, 128, 1, Mode::kPlain>(p, as_stream(stream), "matmul_bf16");
+  if (k == 0) return hipMemsetAsync(c, 0, (size_t)m * n * 2, as_stream(stream)) == hipSuccess
+                         ? KDA_OK : set_error(KDA_ERR_HIP, "matmul_bf16: memset failed");
+  Params p{};
+  p.a = a; p.b = b; p.c = c;
+  p.lda = k; p.ldb = n; p.ldc = n;
+  p.m = (int)m; p.n = (int)n; p.k = (int)k;
+  return launch_auto<true, Epi::kStore>(p, 1, as_stream(stream), "matmul_bf16");
+}
+
+extern "C" int64_t kda_rmsnorm_matmul_bf16_workspace_size(int64_t m, int64_t k) {
+  if (m < 0 || k < 0) return -1;
+  return ((m * k * 2 + 255) / 256) * 256 + m * 4;
 }
 
 extern "C" int kda_rmsnorm_matmul_bf16(const kda_bf16* x, const kda_bf16* gamma, const kda_bf16* w,
                                        kda_bf16* y, int64_t m, int64_t k, int64_t n, float eps,
-                                       void* stream) {
+                                       void* workspace, int64_t workspace_bytes, void* stream) {
   clear_error();
   if (int rc = validate("rmsnorm_matmul_bf16", x, w, y, m, n, k)) return rc;
   if (k == 0) return set_error(KDA_ERR_INVALID_ARG, "rmsnorm_matmul_bf16: K must be > 0");
-  if (!gamma || (reinterpret_cast<uintptr_t>(gamma) & 7))
-    return set_error(KDA_ERR_INVALID_ARG, "rmsnorm_matmul_bf16: gamma null or not 8-byte aligned");
+  if (!gamma || !aligned16(gamma))
+    return set_error(KDA_ERR_INVALID_ARG, "rmsnorm_matmul_bf16: gamma null or not 16-byte aligned");
   if (!(eps >= 0.f)) return set_error(KDA_ERR_INVALID_ARG, "rmsnorm_matmul_bf16: eps must be >= 0");
   if (m == 0 || n == 0) return KDA_OK;
-  Args p{x, w, nullptr, gamma, y, (int)m, (int)n, (int)k, eps};
-  return launch<256, 128, 1, Mode::kRmsNorm>(p, as_stream(stream), "rmsnorm_matmul_bf16");
+  const int64_t need = kda_rmsnorm_matmul_bf16_workspace_size(m, k);
+  if (!workspace || !aligned16(workspace) || workspace_bytes < need)
+    return set_error(KDA_ERR_INVALID_ARG,
+                     "rmsnorm_matmul_bf16: workspace must be 16-byte aligned and >= %lld bytes",
+                     (long long)need);
+  hipStream_t st = as_stream(stream);
+  uint16_t* xg = reinterpret_cast<uint16_t*>(workspace);
+  float* inv = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) +
+                                        ((m * k * 2 + 255) / 256) * 256);
+  hipLaunchKernelGGL(rms_prep_kernel, dim3((unsigned)m), dim3(kPrepThreads), 0, st, x, gamma, xg,
+                     inv, (int)k, eps);
+  if (int rc = check_launch("rmsnorm_matmul_bf16(prep)")) return rc;
+  Params p{};
+  p.a = xg; p.b = w; p.c = y; p.row_scale = inv;
+  p.lda = k; p.ldb = n; p.ldc = n;
+  p.m = (int)m; p.n = (int)n; p.k = (int)k;
+  return launch_auto<true, Epi::kRowScale>(p, 1, st, "rmsnorm_matmul_bf16");
 }
 
 extern "C" int kda_swiglu_bf16(const kda_bf16* x, const kda_bf16* w_up, const kda_bf16* w_down,
@@ -401,9 +543,17 @@ extern "C" int kda_swiglu_bf16(const kda_bf16* x, const kda_bf16* w_up, const kd
   if (!w_up || !aligned16(w_up))
     return set_error(KDA_ERR_INVALID_ARG, "swiglu_bf16: w_up null or misaligned");
   if (m == 0 || k == 0) return KDA_OK;
+  if (f == 0) return hipMemsetAsync(y, 0, (size_t)m * k * 2, as_stream(stream)) == hipSuccess
+                         ? KDA_OK : set_error(KDA_ERR_HIP, "swiglu_bf16: memset failed");
   hipStream_t st = as_stream(stream);
-  Args up{x, w_gate, w_up, nullptr, h, (int)m, (int)f, (int)k, 0.f};
-  if (int rc = launch<256, 64, 2, Mode::kSwiGLU>(up, st, "swiglu_bf16(up/gate)")) return rc;
-  Args down{h, w_down, nullptr, nullptr, y, (int)m, (int)k, (int)f, 0.f};
-  return launch<256, 128, 1, Mode::kPlain>(down, st, "swiglu_bf16(down)");
+  Params up{};
+  up.a = x; up.b = w_gate; up.b2 = w_up; up.c = h;
+  up.lda = k; up.ldb = f; up.ldc = f;
+  up.m = (int)m; up.n = (int)f; up.k = (int)k;
+  if (int rc = launch<256, 128, 2, true, Epi::kSwiGLU>(up, 1, st, "swiglu_bf16(up/gate)")) return rc;
+  Params down{};
+  down.a = h; down.b = w_down; down.c = y;
+  down.lda = f; down.ldb = k; down.ldc = k;
+  down.m = (int)m; down.n = (int)k; down.k = (int)f;
+  return launch_auto<true, Epi::kStore>(down, 1, st, "swiglu_bf16(down)");
 }

@@ -22,16 +22,24 @@ _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
 _int = ctypes.c_int
 
-# name -> argtypes, mirroring include/kda.h one-to-one.  Every entry returns int.
+# name -> argtypes, mirroring include/kda.h one-to-one.  Every entry returns int
+# (a KDA_* status) except those listed in RESTYPES.
 SIGNATURES = {
     "kda_silu_f32": [_p, _p, _i64, _p],
     "kda_adamw_f32": [_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _f32, _f32, _f32, _f32, _i64, _p],
     "kda_rope_f32": [_p, _p, _p, _p, _i64, _i64, _p],
     "kda_matmul_bf16": [_p, _p, _p, _i64, _i64, _i64, _p],
-    "kda_rmsnorm_matmul_bf16": [_p, _p, _p, _p, _i64, _i64, _i64, _f32, _p],
+    "kda_rmsnorm_matmul_bf16": [_p, _p, _p, _p, _i64, _i64, _i64, _f32, _p, _i64, _p],
+    "kda_rmsnorm_matmul_bf16_workspace_size": [_i64, _i64],
     "kda_swiglu_bf16": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "kda_gqa_fwd_bf16": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _int,
                          _i64, _i64, _i64, _p],
+}
+
+
+# Entry points that return something other than an int status.
+RESTYPES = {
+    "kda_rmsnorm_matmul_bf16_workspace_size": _i64,
 }
 
 
@@ -61,7 +69,7 @@ def lib() -> ctypes.CDLL:
         handle.kda_last_error.argtypes = []
         for name, argtypes in SIGNATURES.items():
             fn = getattr(handle, name)  # AttributeError if the symbol is missing
-            fn.restype = _int
+            fn.restype = RESTYPES.get(name, _int)
             fn.argtypes = argtypes
         _LIB = handle
     return _LIB
@@ -76,6 +84,11 @@ def call(name: str, *args) -> None:
         if status in (KDA_ERR_INVALID_ARG, KDA_ERR_UNSUPPORTED):
             raise ValueError(f"{name}: {msg}")
         raise KdaError(name, status, msg)
+
+
+def query(name: str, *args) -> int:
+    """Calls a non-status entry point (a size query) and returns its value."""
+    return int(getattr(lib(), name)(*args))
 
 
 def version() -> int:

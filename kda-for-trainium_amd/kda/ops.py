@@ -24,6 +24,7 @@ __all__ = [
     "rope_single_freq_apply",
     "matmul",
     "rmsnorm_matmul",
+    "rmsnorm_matmul_workspace_size",
     "swiglu",
     "gqa",
 ]
@@ -170,11 +171,14 @@ def matmul(lhs: torch.Tensor, rhs: torch.Tensor) -> torch.Tensor:
 
 
 def rmsnorm_matmul(x: torch.Tensor, w: torch.Tensor, gamma: Optional[torch.Tensor] = None,
-                   eps: float = 0.0) -> torch.Tensor:
-    """out = (x * rsqrt(mean_k(x^2) + eps) * gamma) @ w, fused in one GEMM kernel.
+                   eps: float = 0.0, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out = (x * rsqrt(mean_k(x^2) + eps) * gamma) @ w.
 
     x (M, K), w (K, N), gamma (K,) or None (no gain).  bf16 inputs: bf16 output,
-    fp32 accumulation and fp32 norm statistics.
+    fp32 accumulation and fp32 norm statistics.  A streaming pre-pass writes the
+    per-row 1/rms and bf16(x * gamma) into a workspace (``workspace``: a uint8
+    GPU tensor of at least ``rmsnorm_matmul_workspace_size(M, K)`` bytes, else
+    allocated here); the GEMM applies 1/rms in its epilogue.
     Reference: workspaces/rmsnorm_matmul/runs/rmsnorm_matmul_v1.py:10-138
     (forward x/sqrt(sum(x^2/K)) @ w: gamma=None, eps=0); with gain and eps as in
     workspaces/add_rmsnorm_matmul/runs/offline_bf16_split_sim.py:97-106.
@@ -189,10 +193,21 @@ def rmsnorm_matmul(x: torch.Tensor, w: torch.Tensor, gamma: Optional[torch.Tenso
         gamma = torch.ones(k, dtype=BF16, device=x.device)
     _check("gamma", gamma, BF16, shape=(k,))
     _same_device(x, gamma)
+    need = rmsnorm_matmul_workspace_size(m, k)
+    if workspace is None:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=x.device)
+    _check("workspace", workspace, torch.uint8, ndim=1)
+    _same_device(x, workspace)
     out = torch.empty((m, n), dtype=BF16, device=x.device)
     _lib.call("kda_rmsnorm_matmul_bf16", x.data_ptr(), gamma.data_ptr(), w.data_ptr(),
-              out.data_ptr(), m, k, n, float(eps), _stream(x))
+              out.data_ptr(), m, k, n, float(eps), workspace.data_ptr(), workspace.numel(),
+              _stream(x))
     return out
+
+
+def rmsnorm_matmul_workspace_size(m: int, k: int) -> int:
+    """Bytes of workspace rmsnorm_matmul needs for an (m, k) x."""
+    return _lib.query("kda_rmsnorm_matmul_bf16_workspace_size", int(m), int(k))
 
 
 def swiglu(x: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor, w_gate: torch.Tensor,

@@ -16,7 +16,7 @@ HEADER = ROOT / "include" / "kda.h"
 
 def declared_functions():
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(kda_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(kda_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_header_declares_entry_points():
