@@ -37,13 +37,18 @@
 // Epilogues: plain store; per-row scale (the RMSNorm 1/rms, whose statistics
 // and gamma-scaled bf16 copy of x come from a streaming pre-pass over x, see
 // rms_prep_kernel); SwiGLU (two B operands, silu(gate) * up); fp32 store.
+#include <type_traits>
+
 #include "common.h"
 
 namespace kda {
 namespace gemm {
 
-constexpr int kThreads = 256;
-constexpr int BK = 64;
+constexpr int kWavesM = 2, kWavesN = 4;     // wave grid of a workgroup
+constexpr int kWaves = kWavesM * kWavesN;     // 8 waves: 2 per SIMD
+constexpr int kThreads = 64 * kWaves;
+constexpr int BK = 32;         // k per LDS stage
+constexpr int kStages = 5;     // LDS ring depth (5 x 32 KiB for a 256x256 tile)
 constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
 
@@ -68,9 +73,12 @@ struct Params {
   int m, n, k;
 };
 
-// Position of 16-byte chunk c of row r in a K-contiguous tile (128-byte rows).
-__device__ __forceinline__ int kswz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-// Position of 32-byte segment s of k-row k in an MN-contiguous tile.
+// Position of 16-byte chunk c of row r in a K-contiguous tile (64-byte rows =
+// 4 chunks).  Measured conflict-free for the fragment read (16 consecutive rows,
+// one chunk) at the LDS's 256 B/clk ds_read_b128 rate.
+__device__ __forceinline__ int kswz(int r) { return (r >> 1) & 3; }
+// Position of 32-byte segment s of k-row k in an MN-contiguous tile (measured
+// conflict-free for the ds_read_b64_tr_b16 fragment read).
 __device__ __forceinline__ int mswz(int k) { return (k & 3) | (((k >> 3) & 1) << 2); }
 
 // Maps the linear workgroup id to (tile_m, tile_n): XCD-contiguous, grouped by rows.
@@ -110,17 +118,23 @@ __device__ __forceinline__ void dma16_ptr(const void* src, uint32_t lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
 }
 
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)KDA_LDS_PTR(p);
 }
 
-// Reads the MFMA fragment (column `col`, k = kbase + 8*(lane/16) .. +7) of an
-// MN-contiguous [64][COLS] tile; `col0` is the first column of the 16-column block.
+// Reads the MFMA fragment (column `col0 + lane%16`, k = 8*(lane/16) .. +7) of an
+// MN-contiguous [BK][COLS] tile; col0 is a multiple of 16.
 template <int COLS>
-__device__ __forceinline__ bf16x8 read_mn_frag(const uint8_t* tile, int col0, int kbase, int lane) {
+__device__ __forceinline__ bf16x8 read_mn_frag(const uint8_t* tile, int col0, int lane) {
   const int g = lane >> 4, jj = lane & 15;
   const int s = col0 >> 4;
-  const int k0 = kbase + 8 * g + (jj >> 2);
+  const int k0 = 8 * g + (jj >> 2);
   const int k1 = k0 + 4;
   const uint8_t* p0 = tile + k0 * (2 * COLS) + ((s ^ mswz(k0)) << 5) + 8 * (jj & 3);
   const uint8_t* p1 = tile + k1 * (2 * COLS) + ((s ^ mswz(k1)) << 5) + 8 * (jj & 3);
@@ -133,34 +147,51 @@ __device__ __forceinline__ bf16x8 read_mn_frag(const uint8_t* tile, int col0, in
   return __builtin_bit_cast(bf16x8, v);
 }
 
-// Reads the MFMA fragment (row `row`, k = kbase + 8*(lane/16) .. +7) of a
-// K-contiguous [ROWS][64] tile.
-__device__ __forceinline__ bf16x8 read_k_frag(const uint8_t* tile, int row, int kbase, int lane) {
-  const int c = (kbase >> 3) + (lane >> 4);
-  return *reinterpret_cast<const bf16x8*>(tile + row * 128 + ((c ^ kswz(row)) << 4));
+// Reads the MFMA fragment (row `row`, k = 8*(lane/16) .. +7) of a K-contiguous
+// [ROWS][BK] tile (64-byte rows).
+__device__ __forceinline__ bf16x8 read_k_frag(const uint8_t* tile, int row, int lane) {
+  const int c = lane >> 4;
+  return *reinterpret_cast<const bf16x8*>(tile + row * (BK * 2) + ((c ^ kswz(row)) << 4));
 }
 
-template <int BM, int BN, int NB, bool A_KMAJ, Epi EPI, bool KTAIL>
+// Pipeline: STAGES k-tiles of BK=32 in an LDS ring.  Each wave runs a stream of
+// MFMA groups (one A fragment x all its B fragments) in which the fragments of
+// the next group are always in flight.  Once per k-tile, in the middle of the
+// tile's groups, the wave waits for the DMA of the next k-tile (vmcnt), passes
+// the workgroup barrier (which also proves every wave is done with the stage
+// consumed two tiles ago) and issues the DMA STAGES-1 tiles ahead into that
+// freed stage; the rest of the tile's groups then prefetch the next tile's
+// fragments, so tile boundaries expose neither LDS nor DMA latency.
+template <int BM, int BN, int NB, bool A_KMAJ, Epi EPI, bool KTAIL, int STAGES>
 __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(Params p) {
   static_assert(NB == 1 || NB == 2, "one or two B operands");
   static_assert(BM % 128 == 0 && BN % 128 == 0, "tile");
-  constexpr int WM = BM / 2, WN = BN / 2;     // wave tile (per B operand)
+  static_assert(STAGES >= 3, "ring depth");
+  constexpr int WM = BM / kWavesM, WN = BN / kWavesN;   // wave tile (per B operand)
   constexpr int TM = WM / 16, TN = WN / 16;   // 16x16 MFMA tiles per wave
+  constexpr int NBF = NB * TN;                // B fragments per k-tile per wave
   constexpr int A_BYTES = BM * BK * 2;
   constexpr int B_BYTES = BN * BK * 2;        // per B operand
   constexpr int STAGE = A_BYTES + NB * B_BYTES;
-  constexpr int A_INST = A_BYTES / 1024 / 4;  // DMA instructions per wave per stage
-  constexpr int B_INST = B_BYTES / 1024 / 4;  // ... per B operand
-  constexpr int A_RPI = A_KMAJ ? 8 : 1024 / (2 * BM);  // tile rows per DMA instruction
+  constexpr int A_INST = A_BYTES / 1024 / kWaves;  // DMA instructions per wave per stage
+  constexpr int B_INST = B_BYTES / 1024 / kWaves;  // ... per B operand
+  static_assert(A_INST >= 1 && B_INST >= 1, "DMA split");
+  constexpr int TILE_INST = A_INST + NB * B_INST;
+  constexpr int A_RPI = A_KMAJ ? 1024 / (2 * BK) : 1024 / (2 * BM);  // tile rows per DMA instruction
   constexpr int B_RPI = 1024 / (2 * BN);
-  constexpr int A_LPR = A_KMAJ ? 8 : 2 * BM / 16;       // lanes per tile row
-  constexpr int B_LPR = 2 * BN / 16;
+  constexpr int A_LPR = 64 / A_RPI;           // lanes per tile row
+  constexpr int B_LPR = 64 / B_RPI;
+  constexpr int RA = 4;                       // A fragment ring: prefetch RA-1 groups ahead
+  constexpr int MID = 3;                      // group at which the per-tile barrier sits
+  static_assert(TM % RA == 0 && TM - RA + 1 > MID, "A prefetch ring vs barrier position");
+  constexpr int B_GROUPS = TM - 1 - MID;      // groups that prefetch the next tile's B fragments
+  constexpr int B_PER_GROUP = (NBF + B_GROUPS - 1) / B_GROUPS;
 
   extern __shared__ __align__(1024) uint8_t smem[];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
 
   const int tiles_m = (p.m + BM - 1) / BM, tiles_n = (p.n + BN - 1) / BN;
   int tm, tn;
@@ -181,7 +212,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(Params p) {
   int a_k[A_INST];   // k (within the k-tile) of the lane's data, for the K tail
 #pragma unroll
   for (int j = 0; j < A_INST; ++j) {
-    const int q = j * 4 + wave;
+    const int q = j * kWaves + wave;
     const int r = q * A_RPI + lane / A_LPR;
     const int t = lane % A_LPR;
     if constexpr (A_KMAJ) {
@@ -200,7 +231,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(Params p) {
   int b_k[B_INST];
 #pragma unroll
   for (int j = 0; j < B_INST; ++j) {
-    const int q = j * 4 + wave;
+    const int q = j * kWaves + wave;
     const int r = q * B_RPI + lane / B_LPR;
     const int t = lane % B_LPR;
     const int s = (t >> 1) ^ mswz(r);
@@ -212,26 +243,27 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(Params p) {
   const int64_t b_step = BK * p.ldb * 2;
   const uint32_t lds0 = lds_addr(smem);
 
-  auto issue = [&](int kt, int stage) {
-    const uint32_t base = lds0 + stage * STAGE;
+  // DMA of k-tile `kt` into ring slot `slot % STAGES`.
+  auto issue = [&](int kt, int slot) {
+    const uint32_t base = lds0 + (slot % STAGES) * STAGE;
     const uint8_t* sa = A + kt * a_step;
     const bool tail = KTAIL && (kt + 1) * BK > K;
     if (!tail) {
 #pragma unroll
-      for (int j = 0; j < A_INST; ++j) dma16(sa, a_off[j], base + (j * 4 + wave) * 1024);
+      for (int j = 0; j < A_INST; ++j) dma16(sa, a_off[j], base + (j * kWaves + wave) * 1024);
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         const uint8_t* sb = Bop[b] + kt * b_step;
 #pragma unroll
         for (int j = 0; j < B_INST; ++j)
-          dma16(sb, b_off[j], base + A_BYTES + b * B_BYTES + (j * 4 + wave) * 1024);
+          dma16(sb, b_off[j], base + A_BYTES + b * B_BYTES + (j * kWaves + wave) * 1024);
       }
     } else {
       const int kbase = kt * BK;
 #pragma unroll
       for (int j = 0; j < A_INST; ++j) {
         const void* src = (kbase + a_k[j] < K) ? (const void*)(sa + a_off[j]) : (const void*)g_zero_chunk;
-        dma16_ptr(src, base + (j * 4 + wave) * 1024);
+        dma16_ptr(src, base + (j * kWaves + wave) * 1024);
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
@@ -239,12 +271,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(Params p) {
 #pragma unroll
         for (int j = 0; j < B_INST; ++j) {
           const void* src = (kbase + b_k[j] < K) ? (const void*)(sb + b_off[j]) : (const void*)g_zero_chunk;
-          dma16_ptr(src, base + A_BYTES + b * B_BYTES + (j * 4 + wave) * 1024);
+          dma16_ptr(src, base + A_BYTES + b * B_BYTES + (j * kWaves + wave) * 1024);
         }
       }
     }
   };
-
   floatx4 acc[NB][TM][TN];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
@@ -253,65 +284,79 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(Params p) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) acc[b][i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // Fragment readers for one 32-wide k half (kh) of the current stage.
-  auto read_a = [&](const uint8_t* at, int kh, int i) -> bf16x8 {
+  auto stage_ptr = [&](int kt) -> const uint8_t* { return smem + (kt % STAGES) * STAGE; };
+  auto read_a = [&](int kt, int i) -> bf16x8 {
+    const uint8_t* at = stage_ptr(kt);
     if constexpr (A_KMAJ)
-      return read_k_frag(at, wm * WM + i * 16 + (lane & 15), kh * 32, lane);
+      return read_k_frag(at, wm * WM + i * 16 + (lane & 15), lane);
     else
-      return read_mn_frag<BM>(at, wm * WM + i * 16, kh * 32, lane);
+      return read_mn_frag<BM>(at, wm * WM + i * 16, lane);
   };
-  auto read_b = [&](const uint8_t* bt, int kh, int bj) -> bf16x8 {
+  auto read_b = [&](int kt, int bj) -> bf16x8 {
     const int b = bj / TN, j = bj % TN;
-    return read_mn_frag<BN>(bt + b * B_BYTES, wn * WN + j * 16, kh * 32, lane);
+    return read_mn_frag<BN>(stage_ptr(kt) + A_BYTES + b * B_BYTES, wn * WN + j * 16, lane);
   };
-  constexpr int KH = BK / 32;               // k halves per stage
-  constexpr int NBF = NB * TN;              // B fragments per k half
-  static_assert(NBF % TM == 0 || TM % NBF == 0, "B prefetch split");
-  constexpr int B_PER_GROUP = (NBF + TM - 1) / TM;
 
-  issue(0, 0);
-  for (int kt = 0; kt < nk; ++kt) {
-    const int stage = kt & 1;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    if (kt + 1 < nk) issue(kt + 1, stage ^ 1);
-    const uint8_t* at = smem + stage * STAGE;
-    const uint8_t* bt = at + A_BYTES;
-    // Software pipeline over MFMA groups g = (kh, i): group g multiplies A
-    // fragment i against the NB*TN B fragments of half kh, while the A fragment
-    // of group g+1 and a slice of the next half's B fragments are in flight.
-    bf16x8 af[2], bfr[2][NBF];
+  // ---- prologue: tiles 0 .. STAGES-2 in flight; tile 0 published.  Tile
+  // indices past the last k-tile are clamped to it: those DMAs re-read valid
+  // memory into stages that are no longer needed, so the steady state issues
+  // and waits for exactly STAGES-1 tiles ahead with no data-dependent branches.
 #pragma unroll
-    for (int bj = 0; bj < NBF; ++bj) bfr[0][bj] = read_b(bt, 0, bj);
-    af[0] = read_a(at, 0, 0);
+  for (int t = 0; t < STAGES - 1; ++t) issue(min(t, nk - 1), t);
+  wait_vmcnt<(STAGES - 2) * TILE_INST>();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  bf16x8 af[RA], bfr[2][NBF];
 #pragma unroll
-    for (int kh = 0; kh < KH; ++kh) {
+  for (int bj = 0; bj < NBF; ++bj) bfr[0][bj] = read_b(0, bj);
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int g = kh * TM + i;
-        if (i + 1 < TM)
-          af[(g + 1) & 1] = read_a(at, kh, i + 1);
-        else if (kh + 1 < KH)
-          af[(g + 1) & 1] = read_a(at, kh + 1, 0);
-        if (kh + 1 < KH) {
+  for (int d = 0; d < RA - 1; ++d) af[d] = read_a(0, d);
+
+  // One k-tile of MFMA groups (group i = A fragment i x the NB*TN B fragments).
+  // CUR, the tile's parity, selects the B fragment buffer at compile time so the
+  // fragment arrays stay in registers.  Group i reads the A fragment of group
+  // i+RA-1 (possibly of the next tile) and, after the barrier, a slice of the
+  // next tile's B fragments.  On the last tile these prefetches read a stage
+  // holding stale data; the values are never used.
+  auto tile_body = [&](int kt, auto cur_c) {
+    constexpr int CUR = decltype(cur_c)::value;
 #pragma unroll
-          for (int u = 0; u < B_PER_GROUP; ++u) {
-            const int bj = i * B_PER_GROUP + u;
-            if (bj < NBF) bfr[(kh + 1) & 1][bj] = read_b(bt, kh + 1, bj);
-          }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int b = 0; b < NB; ++b)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-            acc[b][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[kh & 1][b * TN + j], af[g & 1],
-                                                                   acc[b][i][j], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < TM; ++i) {
+      if (i == MID) {
+        wait_vmcnt<(STAGES - 3) * TILE_INST>();
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        issue(min(kt + STAGES - 1, nk - 1), kt + STAGES - 1);
       }
+      const int ga = i + RA - 1;
+      if (ga < TM)
+        af[ga % RA] = read_a(kt, ga);
+      else
+        af[ga % RA] = read_a(kt + 1, ga - TM);
+      if (i >= MID && i < MID + B_GROUPS) {
+#pragma unroll
+        for (int u = 0; u < B_PER_GROUP; ++u) {
+          const int bj = (i - MID) * B_PER_GROUP + u;
+          if (bj < NBF) bfr[CUR ^ 1][bj] = read_b(kt + 1, bj);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[b][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[CUR][b * TN + j], af[i % RA],
+                                                                 acc[b][i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  for (int kt = 0; kt < nk; kt += 2) {
+    tile_body(kt, std::integral_constant<int, 0>{});
+    if (kt + 1 < nk) tile_body(kt + 1, std::integral_constant<int, 1>{});
   }
+  // No DMA may still be writing this workgroup's LDS when it exits.
+  wait_vmcnt<0>();
 
   // ---- epilogue: lane holds C[row][col .. col+3] for each 16x16 tile
   const int col_in = (lane >> 4) * 4;
@@ -429,24 +474,25 @@ __global__ __launch_bounds__(kPrepThreads) void rms_prep_kernel(const uint16_t* 
 
 template <int BM, int BN, int NB, bool A_KMAJ, Epi EPI>
 int launch(const Params& a, int batch, hipStream_t st, const char* what) {
+  constexpr int S = kStages;
   const int tiles = ((a.m + BM - 1) / BM) * ((a.n + BN - 1) / BN);
-  const size_t lds = (size_t)2 * (BM + NB * BN) * BK * sizeof(uint16_t);
+  const size_t lds = (size_t)S * (BM + NB * BN) * BK * sizeof(uint16_t);
   static const bool attr_ok = [&] {
     const hipError_t e1 = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, false>),
+        reinterpret_cast<const void*>(gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, false, S>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     const hipError_t e2 = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, true>),
+        reinterpret_cast<const void*>(gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, true, S>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     return e1 == hipSuccess && e2 == hipSuccess;
   }();
   if (!attr_ok) return set_error(KDA_ERR_HIP, "%s: cannot reserve %zu bytes of LDS", what, lds);
   const dim3 grid(tiles, batch);
   if (a.k % BK == 0)
-    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, false>), grid, dim3(kThreads),
+    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, false, S>), grid, dim3(kThreads),
                        lds, st, a);
   else
-    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, true>), grid, dim3(kThreads),
+    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, true, S>), grid, dim3(kThreads),
                        lds, st, a);
   return check_launch(what);
 }
