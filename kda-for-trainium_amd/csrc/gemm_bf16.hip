@@ -47,8 +47,8 @@ namespace gemm {
 constexpr int kWavesM = 2, kWavesN = 4;     // wave grid of a workgroup
 constexpr int kWaves = kWavesM * kWavesN;     // 8 waves: 2 per SIMD
 constexpr int kThreads = 64 * kWaves;
-constexpr int BK = 32;         // k per LDS stage
-constexpr int kStages = 5;     // LDS ring depth (5 x 32 KiB for a 256x256 tile)
+constexpr int kBK = 32;        // k per LDS slot
+constexpr int kStages = 4;     // LDS slots (4 x 32 KiB for a 256x256 tile)
 constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
 
@@ -73,10 +73,12 @@ struct Params {
   int m, n, k;
 };
 
-// Position of 16-byte chunk c of row r in a K-contiguous tile (64-byte rows =
-// 4 chunks).  Measured conflict-free for the fragment read (16 consecutive rows,
+// Position of 16-byte chunk c of row r in a K-contiguous tile of BK-element
+// rows: 64-byte rows (BK=32, 4 chunks) or 128-byte rows (BK=64, 8 chunks).
+// Both are measured conflict-free for the fragment read (16 consecutive rows,
 // one chunk) at the LDS's 256 B/clk ds_read_b128 rate.
-__device__ __forceinline__ int kswz(int r) { return (r >> 1) & 3; }
+template <int BK>
+__device__ __forceinline__ int kswz(int r) { return BK == 32 ? ((r >> 1) & 3) : (r & 7); }
 // Position of 32-byte segment s of k-row k in an MN-contiguous tile (measured
 // conflict-free for the ds_read_b64_tr_b16 fragment read).
 __device__ __forceinline__ int mswz(int k) { return (k & 3) | (((k >> 3) & 1) << 2); }
@@ -128,13 +130,13 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)KDA_LDS_PTR(p);
 }
 
-// Reads the MFMA fragment (column `col0 + lane%16`, k = 8*(lane/16) .. +7) of an
+// Reads the MFMA fragment (column `col0 + lane%16`, k = kbase + 8*(lane/16) .. +7) of an
 // MN-contiguous [BK][COLS] tile; col0 is a multiple of 16.
 template <int COLS>
-__device__ __forceinline__ bf16x8 read_mn_frag(const uint8_t* tile, int col0, int lane) {
+__device__ __forceinline__ bf16x8 read_mn_frag(const uint8_t* tile, int col0, int kbase, int lane) {
   const int g = lane >> 4, jj = lane & 15;
   const int s = col0 >> 4;
-  const int k0 = 8 * g + (jj >> 2);
+  const int k0 = kbase + 8 * g + (jj >> 2);
   const int k1 = k0 + 4;
   const uint8_t* p0 = tile + k0 * (2 * COLS) + ((s ^ mswz(k0)) << 5) + 8 * (jj & 3);
   const uint8_t* p1 = tile + k1 * (2 * COLS) + ((s ^ mswz(k1)) << 5) + 8 * (jj & 3);
@@ -147,11 +149,12 @@ __device__ __forceinline__ bf16x8 read_mn_frag(const uint8_t* tile, int col0, in
   return __builtin_bit_cast(bf16x8, v);
 }
 
-// Reads the MFMA fragment (row `row`, k = 8*(lane/16) .. +7) of a K-contiguous
-// [ROWS][BK] tile (64-byte rows).
-__device__ __forceinline__ bf16x8 read_k_frag(const uint8_t* tile, int row, int lane) {
-  const int c = lane >> 4;
-  return *reinterpret_cast<const bf16x8*>(tile + row * (BK * 2) + ((c ^ kswz(row)) << 4));
+// Reads the MFMA fragment (row `row`, k = kbase + 8*(lane/16) .. +7) of a
+// K-contiguous [ROWS][BK] tile (128-byte rows).
+template <int BK>
+__device__ __forceinline__ bf16x8 read_k_frag(const uint8_t* tile, int row, int kbase, int lane) {
+  const int c = (kbase >> 3) + (lane >> 4);
+  return *reinterpret_cast<const bf16x8*>(tile + row * (BK * 2) + ((c ^ kswz<BK>(row)) << 4));
 }
 
 // Pipeline: STAGES k-tiles of BK=32 in an LDS ring.  Each wave runs a stream of
@@ -162,11 +165,11 @@ __device__ __forceinline__ bf16x8 read_k_frag(const uint8_t* tile, int row, int 
 // consumed two tiles ago) and issues the DMA STAGES-1 tiles ahead into that
 // freed stage; the rest of the tile's groups then prefetch the next tile's
 // fragments, so tile boundaries expose neither LDS nor DMA latency.
-template <int BM, int BN, int NB, bool A_KMAJ, Epi EPI, bool KTAIL, int STAGES>
+template <int BM, int BN, int NB, bool A_KMAJ, Epi EPI, bool KTAIL, int BK, int STAGES>
 __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(Params p) {
   static_assert(NB == 1 || NB == 2, "one or two B operands");
   static_assert(BM % 128 == 0 && BN % 128 == 0, "tile");
-  static_assert(STAGES >= 3, "ring depth");
+  static_assert(STAGES >= 2, "ring depth");
   constexpr int WM = BM / kWavesM, WN = BN / kWavesN;   // wave tile (per B operand)
   constexpr int TM = WM / 16, TN = WN / 16;   // 16x16 MFMA tiles per wave
   constexpr int NBF = NB * TN;                // B fragments per k-tile per wave
@@ -181,11 +184,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(Params p) {
   constexpr int B_RPI = 1024 / (2 * BN);
   constexpr int A_LPR = 64 / A_RPI;           // lanes per tile row
   constexpr int B_LPR = 64 / B_RPI;
-  constexpr int RA = 4;                       // A fragment ring: prefetch RA-1 groups ahead
-  constexpr int MID = 3;                      // group at which the per-tile barrier sits
-  static_assert(TM % RA == 0 && TM - RA + 1 > MID, "A prefetch ring vs barrier position");
-  constexpr int B_GROUPS = TM - 1 - MID;      // groups that prefetch the next tile's B fragments
-  constexpr int B_PER_GROUP = (NBF + B_GROUPS - 1) / B_GROUPS;
+  static_assert(kWaves == 8, "ping-pong needs 8 waves");
 
   extern __shared__ __align__(1024) uint8_t smem[];
 
@@ -216,7 +215,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(Params p) {
     const int r = q * A_RPI + lane / A_LPR;
     const int t = lane % A_LPR;
     if constexpr (A_KMAJ) {
-      const int c = t ^ kswz(r);
+      const int c = t ^ kswz<BK>(r);
       const int gm = min(m0 + r, M - 1);
       a_off[j] = (uint32_t)(((int64_t)gm * p.lda + 8 * c) * 2);
       a_k[j] = 8 * c;
@@ -285,75 +284,92 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(Params p) {
       for (int j = 0; j < TN; ++j) acc[b][i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   auto stage_ptr = [&](int kt) -> const uint8_t* { return smem + (kt % STAGES) * STAGE; };
-  auto read_a = [&](int kt, int i) -> bf16x8 {
+  auto read_a = [&](int kt, int kh, int i) -> bf16x8 {
     const uint8_t* at = stage_ptr(kt);
     if constexpr (A_KMAJ)
-      return read_k_frag(at, wm * WM + i * 16 + (lane & 15), lane);
+      return read_k_frag<BK>(at, wm * WM + i * 16 + (lane & 15), kh * 32, lane);
     else
-      return read_mn_frag<BM>(at, wm * WM + i * 16, lane);
+      return read_mn_frag<BM>(at, wm * WM + i * 16, kh * 32, lane);
   };
-  auto read_b = [&](int kt, int bj) -> bf16x8 {
+  auto read_b = [&](int kt, int kh, int bj) -> bf16x8 {
     const int b = bj / TN, j = bj % TN;
-    return read_mn_frag<BN>(stage_ptr(kt) + A_BYTES + b * B_BYTES, wn * WN + j * 16, lane);
+    return read_mn_frag<BN>(stage_ptr(kt) + A_BYTES + b * B_BYTES, wn * WN + j * 16, kh * 32, lane);
   };
 
-  // ---- prologue: tiles 0 .. STAGES-2 in flight; tile 0 published.  Tile
-  // indices past the last k-tile are clamped to it: those DMAs re-read valid
-  // memory into stages that are no longer needed, so the steady state issues
-  // and waits for exactly STAGES-1 tiles ahead with no data-dependent branches.
-#pragma unroll
-  for (int t = 0; t < STAGES - 1; ++t) issue(min(t, nk - 1), t);
-  wait_vmcnt<(STAGES - 2) * TILE_INST>();
+  // ---- ping-pong schedule.  Waves 0-3 (group 0) and 4-7 (group 1) hold one
+  // wave per SIMD each and run the same program one phase apart: while one
+  // group issues the back-to-back MFMAs of a k-tile (raised priority), the
+  // other reads the fragments of its next k-tile from LDS and issues its share
+  // of the DMA two k-tiles ahead.  One workgroup barrier per phase:
+  //   phase 2t:   group 0 loads tile t     group 1 computes tile t-1
+  //   phase 2t+1: group 0 computes tile t  group 1 loads tile t
+  // Tile t must be in LDS before phase 2t.  Each wave issues its share while
+  // loading tile t-2 (group 0: phase 2t-4, group 1: 2t-3) and awaits it at the
+  // end of phase 2t-1, with only its share of tile t+1 allowed in flight.  The
+  // DMA of tile t+2 overwrites the slot of tile t+2-STAGES, whose last reader
+  // (group 1) finished in phase 2t+5-2*STAGES < 2t.  Tile indices past the last
+  // k-tile are clamped: those DMAs re-read valid memory into unused slots.
+  // LEAD = how many k-tiles ahead the DMA runs: 2 with >= 3 slots (each wave
+  // issues while loading; group 1's share of tile t is awaited at the end of
+  // phase 2t-1 with tile t+1 in flight), 1 with 2 slots (every wave issues its
+  // share of tile t+1 at the start of phase 2t -- group 0 while loading, group 1
+  // while computing -- into the slot of tile t-1, whose last reader finished in
+  // phase 2t-1, and awaits it at the end of phase 2t+1).
+  constexpr int LEAD = STAGES >= 3 ? 2 : 1;
+  constexpr int KH = BK / 32;                   // 32-wide k halves per tile
+  const int grp = wave >> 2;
+  issue(0, 0);
+  if constexpr (LEAD == 2) {
+    issue(min(1, nk - 1), 1);
+    wait_vmcnt<TILE_INST>();
+  } else {
+    wait_vmcnt<0>();
+  }
   __builtin_amdgcn_s_barrier();
+  if (grp == 1) {
+    if constexpr (LEAD == 1) issue(min(1, nk - 1), 1);
+    __builtin_amdgcn_s_barrier();   // group 1 starts one phase later
+  }
   asm volatile("" ::: "memory");
 
-  bf16x8 af[RA], bfr[2][NBF];
+  bf16x8 af[KH][TM], bfr[KH][NBF];
+  for (int kt = 0; kt < nk; ++kt) {
+    // -- load phase: fragments of tile kt
+    if (LEAD == 2 || grp == 0) issue(min(kt + LEAD, nk - 1), kt + LEAD);
 #pragma unroll
-  for (int bj = 0; bj < NBF; ++bj) bfr[0][bj] = read_b(0, bj);
+    for (int kh = 0; kh < KH; ++kh) {
 #pragma unroll
-  for (int d = 0; d < RA - 1; ++d) af[d] = read_a(0, d);
-
-  // One k-tile of MFMA groups (group i = A fragment i x the NB*TN B fragments).
-  // CUR, the tile's parity, selects the B fragment buffer at compile time so the
-  // fragment arrays stay in registers.  Group i reads the A fragment of group
-  // i+RA-1 (possibly of the next tile) and, after the barrier, a slice of the
-  // next tile's B fragments.  On the last tile these prefetches read a stage
-  // holding stale data; the values are never used.
-  auto tile_body = [&](int kt, auto cur_c) {
-    constexpr int CUR = decltype(cur_c)::value;
+      for (int i = 0; i < TM; ++i) af[kh][i] = read_a(kt, kh, i);
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      if (i == MID) {
-        wait_vmcnt<(STAGES - 3) * TILE_INST>();
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        issue(min(kt + STAGES - 1, nk - 1), kt + STAGES - 1);
-      }
-      const int ga = i + RA - 1;
-      if (ga < TM)
-        af[ga % RA] = read_a(kt, ga);
-      else
-        af[ga % RA] = read_a(kt + 1, ga - TM);
-      if (i >= MID && i < MID + B_GROUPS) {
-#pragma unroll
-        for (int u = 0; u < B_PER_GROUP; ++u) {
-          const int bj = (i - MID) * B_PER_GROUP + u;
-          if (bj < NBF) bfr[CUR ^ 1][bj] = read_b(kt + 1, bj);
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[b][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[CUR][b * TN + j], af[i % RA],
-                                                                 acc[b][i][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
+      for (int bj = 0; bj < NBF; ++bj) bfr[kh][bj] = read_b(kt, kh, bj);
     }
-  };
-  for (int kt = 0; kt < nk; kt += 2) {
-    tile_body(kt, std::integral_constant<int, 0>{});
-    if (kt + 1 < nk) tile_body(kt + 1, std::integral_constant<int, 1>{});
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (grp == 1) {
+      if constexpr (LEAD == 2) wait_vmcnt<TILE_INST>();
+      else wait_vmcnt<0>();
+    }
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    // -- compute phase
+    if (LEAD == 1 && grp == 1 && kt + 2 < nk + 1) issue(min(kt + 2, nk - 1), kt + 2);
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int kh = 0; kh < KH; ++kh)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[b][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[kh][b * TN + j], af[kh][i],
+                                                                   acc[b][i][j], 0, 0, 0);
+    __builtin_amdgcn_s_setprio(0);
+    if (grp == 0) {
+      if constexpr (LEAD == 2) wait_vmcnt<TILE_INST>();
+      else wait_vmcnt<0>();
+    }
+    if (!(grp == 1 && kt + 1 == nk)) __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
   }
   // No DMA may still be writing this workgroup's LDS when it exits.
   wait_vmcnt<0>();
@@ -472,27 +488,26 @@ __global__ __launch_bounds__(kPrepThreads) void rms_prep_kernel(const uint16_t* 
 
 // ---------------------------------------------------------------- launch helpers
 
-template <int BM, int BN, int NB, bool A_KMAJ, Epi EPI>
+template <int BM, int BN, int NB, bool A_KMAJ, Epi EPI, int BK = kBK, int S = kStages>
 int launch(const Params& a, int batch, hipStream_t st, const char* what) {
-  constexpr int S = kStages;
   const int tiles = ((a.m + BM - 1) / BM) * ((a.n + BN - 1) / BN);
   const size_t lds = (size_t)S * (BM + NB * BN) * BK * sizeof(uint16_t);
   static const bool attr_ok = [&] {
     const hipError_t e1 = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, false, S>),
+        reinterpret_cast<const void*>(gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, false, BK, S>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     const hipError_t e2 = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, true, S>),
+        reinterpret_cast<const void*>(gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, true, BK, S>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     return e1 == hipSuccess && e2 == hipSuccess;
   }();
   if (!attr_ok) return set_error(KDA_ERR_HIP, "%s: cannot reserve %zu bytes of LDS", what, lds);
   const dim3 grid(tiles, batch);
   if (a.k % BK == 0)
-    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, false, S>), grid, dim3(kThreads),
+    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, false, BK, S>), grid, dim3(kThreads),
                        lds, st, a);
   else
-    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, true, S>), grid, dim3(kThreads),
+    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, NB, A_KMAJ, EPI, true, BK, S>), grid, dim3(kThreads),
                        lds, st, a);
   return check_launch(what);
 }
