@@ -73,6 +73,27 @@ int kda_adamw_f32(const float* param_in, const float* grad, const float* m_in,
 int kda_rope_f32(const float* x, const float* cos_t, const float* sin_t, float* out,
                  int64_t d, int64_t s, void* stream);
 
+/* ---------------------------------------------------------------- workspaces
+ * Entry points that stage intermediates (bf16 hi/lo planes of fp32 operands,
+ * normalised activations, row statistics) take a caller-owned device buffer
+ * `workspace` of at least kda_workspace_size(op, ...) bytes, 16-byte aligned.
+ * The library never allocates. */
+enum {
+  KDA_OP_MATMUL_F32 = 1,
+  KDA_OP_TRANSPOSE_MATMUL_F32 = 2,
+  KDA_OP_BMM_F32 = 3,
+  KDA_OP_LORA_F32 = 4,
+  KDA_OP_RMSNORM_MATMUL_F32 = 5,
+  KDA_OP_ADD_RMSNORM_MATMUL_F32 = 6,
+  KDA_OP_MATMUL_ADD_RMSNORM_F32 = 7,
+  KDA_OP_SWIGLU_F32 = 8,          /* n = F (intermediate width) */
+  KDA_OP_RMSNORM_MATMUL_BF16 = 9
+};
+
+/* Workspace bytes for operator `op` at the given sizes (unused sizes: 0);
+ * -1 for an unknown op or a negative size. */
+int64_t kda_workspace_size(int op, int64_t batch, int64_t m, int64_t k, int64_t n, int64_t r);
+
 /* ---------------------------------------------------------------- bf16 GEMMs
  * bf16 storage, fp32 accumulation on MFMA, bf16 output.  Shape limits: K and N
  * multiples of 8 (16-byte rows); all pointers 16-byte aligned; any M. */
@@ -85,17 +106,13 @@ int kda_matmul_bf16(const kda_bf16* a, const kda_bf16* b, kda_bf16* c, int64_t m
 /* y[M,N] = (x * rsqrt(mean_k(x^2) + eps) * gamma) @ w, x [M,K], gamma [K] (16-byte
  * aligned), w [K,N].  A streaming pre-pass reads x once and writes the per-row
  * 1/rms (fp32) and bf16(x * gamma) into `workspace`; the GEMM applies 1/rms to
- * its accumulators in the epilogue.  `workspace` is caller-owned device memory
- * of at least kda_rmsnorm_matmul_bf16_workspace_size(m, k) bytes, 16-byte aligned.
+ * its accumulators in the epilogue.  Workspace: KDA_OP_RMSNORM_MATMUL_BF16.
  * Replaces kernel(v1=x, v2=w) of workspaces/rmsnorm_matmul/runs/rmsnorm_matmul_v1.py:10-138
  * (which has no gain and no eps) and the x+z-free part of
  * workspaces/add_rmsnorm_matmul/runs/add_rmsnorm_matmul_v1.py:8-146 (gain g, eps). */
 int kda_rmsnorm_matmul_bf16(const kda_bf16* x, const kda_bf16* gamma, const kda_bf16* w,
                             kda_bf16* y, int64_t m, int64_t k, int64_t n, float eps,
                             void* workspace, int64_t workspace_bytes, void* stream);
-
-/* Bytes of workspace kda_rmsnorm_matmul_bf16 needs for an [m, k] x (-1 if negative). */
-int64_t kda_rmsnorm_matmul_bf16_workspace_size(int64_t m, int64_t k);
 
 /* y[M,K] = (silu(x @ w_gate) * (x @ w_up)) @ w_down with x [M,K], w_up/w_gate [K,F],
  * w_down [F,K].  h is caller-provided scratch of M*F bf16 (the gated activation,
@@ -104,6 +121,64 @@ int64_t kda_rmsnorm_matmul_bf16_workspace_size(int64_t m, int64_t k);
 int kda_swiglu_bf16(const kda_bf16* x, const kda_bf16* w_up, const kda_bf16* w_down,
                     const kda_bf16* w_gate, kda_bf16* h, kda_bf16* y, int64_t m, int64_t k,
                     int64_t f, void* stream);
+
+/* ---------------------------------------------------------------- fp32 GEMMs
+ * The reference's fp32 NKIBench operators.  fp32 in, fp32 out, computed on bf16
+ * MFMA through a three-product split (x = hi + lo in bf16; A@B ~= Ah@Bh + Ah@Bl +
+ * Al@Bh, fp32 accumulation; relative-L2 ~5e-6 on N(0,1) data), the same scheme
+ * as workspaces/matmul/runs/matmul_v3_bf16_split.py:21-33.  K (and every
+ * contraction extent) must be a multiple of 32, N a multiple of 8; pointers
+ * 16-byte aligned.  All arrays dense row-major. */
+
+/* out[M,N] = lhs[M,K] @ rhs[K,N].  Replaces kernel(v1=lhs, v2=rhs) of
+ * workspaces/matmul/runs/matmul_v3_bf16_split.py:10-161 (forward lhs @ rhs). */
+int kda_matmul_f32(const float* lhs, const float* rhs, float* out, int64_t m, int64_t k,
+                   int64_t n, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* out[M,N] = lhs^T @ rhs with lhs [K,M], rhs [K,N]; M a multiple of 8.  Replaces
+ * kernel(v1=lhs, v2=rhs) of workspaces/transpose_matmul/runs/tmm_v3_mblk16_bf16_split.py:10-41
+ * (forward transpose(lhs) @ rhs). */
+int kda_transpose_matmul_f32(const float* lhs, const float* rhs, float* out, int64_t m,
+                             int64_t k, int64_t n, void* workspace, int64_t workspace_bytes,
+                             void* stream);
+
+/* out[b] = lhs[b] @ rhs[b], lhs [B,M,K], rhs [B,K,N], out [B,M,N].  Replaces
+ * kernel(lhs, rhs) of workspaces/bmm/runs/bmm_v2.py:10-41. */
+int kda_bmm_f32(const float* lhs, const float* rhs, float* out, int64_t batch, int64_t m,
+                int64_t k, int64_t n, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* out[M,N] = x[M,K] @ w[K,N] + (x @ a[K,R]) @ b[R,N], both terms in one
+ * accumulation.  Replaces kernel(x, w, a, b) of workspaces/lora/runs/lora_v3_bf16_split.py:10-64. */
+int kda_lora_f32(const float* x, const float* w, const float* a, const float* b, float* out,
+                 int64_t m, int64_t k, int64_t n, int64_t r, void* workspace,
+                 int64_t workspace_bytes, void* stream);
+
+/* out[M,N] = (x / sqrt(sum_k(x^2 / K))) @ w (no eps, no gain).  Replaces
+ * kernel(v1=x, v2=w) of workspaces/rmsnorm_matmul/runs/rmsnorm_matmul_v1.py:10-138. */
+int kda_rmsnorm_matmul_f32(const float* x, const float* w, float* out, int64_t m, int64_t k,
+                           int64_t n, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* y = x + z; out[M,N] = (y / sqrt(sum_k(y^2 / K) + eps) * g) @ w with x, z [M,K],
+ * g [K], w [K,N].  Argument order of forward(x, w, eps, z, g) /
+ * workspaces/add_rmsnorm_matmul/runs/add_rmsnorm_matmul_v1.py:8-146. */
+int kda_add_rmsnorm_matmul_f32(const float* x, const float* w, float eps, const float* z,
+                               const float* g, float* out, int64_t m, int64_t k, int64_t n,
+                               void* workspace, int64_t workspace_bytes, void* stream);
+
+/* y = x @ w + z; out[M,N] = y * g / sqrt(mean_n(y^2) + eps) with x [M,K], w [K,N],
+ * z [M,N], g [N].  The GEMM epilogue adds z and writes per-row partial sums of
+ * squares; a row kernel applies the norm in place.  Argument order of
+ * forward(x, w, eps, z, g) / workspaces/matmul_add_rmsnorm/runs/matmul_add_rmsnorm_v2_bf16_split.py:8-212. */
+int kda_matmul_add_rmsnorm_f32(const float* x, const float* w, float eps, const float* z,
+                               const float* g, float* out, int64_t m, int64_t k, int64_t n,
+                               void* workspace, int64_t workspace_bytes, void* stream);
+
+/* out[M,K] = (silu(x @ w_gate) * (x @ w_up)) @ w_down, fp32, x [M,K], w_up/w_gate
+ * [K,F], w_down [F,K]; workspace KDA_OP_SWIGLU_F32 with n = F.  Argument order of
+ * kernel(v1=x, v2=w_up, v3=w_down, v4=w_gate) of workspaces/swiglu/runs/swiglu_v1.py:38-146. */
+int kda_swiglu_f32(const float* x, const float* w_up, const float* w_down, const float* w_gate,
+                   float* out, int64_t m, int64_t k, int64_t f, void* workspace,
+                   int64_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------- attention */
 

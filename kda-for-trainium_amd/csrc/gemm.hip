@@ -1,0 +1,1194 @@
+// GEMM family on gfx950 bf16 MFMA (v_mfma_f32_16x16x32_bf16), fp32 accumulation.
+//
+//   C[M,N] = sum over K-segments s of  A_s[M,K_s] @ B_s[K_s,N]
+//
+// One kernel template serves every GEMM-shaped operator of the library:
+//   * bf16 operands (graded RMSNorm->matmul and SwiGLU configurations, bf16 matmul);
+//   * fp32 operands through a three-product bf16 split: x = hi + lo with hi =
+//     bf16(x), lo = bf16(x - hi), and A@B ~= Ah@Bh + Ah@Bl + Al@Bh, expressed as
+//     three K-segments (Ah,Bh), (Ah,Bl), (Al,Bh) over bf16 planes written by a
+//     streaming pre-pass (split_f32_kernel).  The dropped Al@Bl term is ~2^-16
+//     relative per product; fp32 accumulation throughout;
+//   * LoRA x@w + (x@a)@b as six segments (the split x@w plus the split t@b);
+//   * batched products (blockIdx.y = batch, per-batch strides).
+//
+// Data path (one 256 x BN output tile per workgroup, 8 waves in a 2 x 4 grid,
+// each wave owning a 128 x BN/4 fp32 accumulator block):
+//
+//   HBM --global_load_lds_dwordx4--> LDS (4-slot ring of BK=32 k-tiles) --ds_read--> MFMA
+//
+//   * Operands go straight from global memory into LDS, 16 bytes per lane with
+//     no register staging: each wave instruction fills 1 KiB of LDS lane-
+//     linearly, so the LDS swizzle is applied on the global side by choosing
+//     which 16-byte chunk each lane fetches.  The DMA is inline asm so the
+//     compiler does not serialise later LDS reads behind it; completion is
+//     awaited explicitly (s_waitcnt vmcnt) before the barrier that publishes a slot.
+//   * K-contiguous operands (A row-major) are stored [rows][32 k] (64-byte
+//     rows), chunk c of row r at c ^ ((r >> 1) & 3): one ds_read_b128 gives an
+//     MFMA fragment (one row, 8 consecutive k).
+//   * MN-contiguous operands (B row-major [K][N], or A stored [K][M]) keep their
+//     HBM orientation, [32 k][cols], 32-byte segment s of k-row k at s ^ mswz(k).
+//     A fragment (one column, 8 consecutive k) is read with two
+//     ds_read_b64_tr_b16: within a 16-lane group, lane 4r+q names 4 elements of
+//     k-row r and lane j receives column j of that 4 x 16 block.
+//   * Both layouts were measured bank-conflict free (256 B/clk) on this LDS.
+//   * Ping-pong schedule: waves 0-3 and 4-7 (one wave per SIMD each) run one
+//     phase apart, so that while one group issues the back-to-back MFMAs of a
+//     k-tile the other reads its next fragments and issues DMA two tiles ahead.
+//
+// MFMA operand order: the B fragment is the MFMA "A" operand and the A fragment
+// the "B" operand, so each lane's 4 accumulators are 4 consecutive columns of
+// one output row (8-byte bf16 or 16-byte fp32 stores).
+//
+// Tile order: workgroups are dealt round-robin to the 8 XCDs, so consecutive
+// tile ids are remapped onto one XCD (sharing its L2), then walked in groups of
+// kGroupM tile-rows so co-resident tiles reuse the same A rows and B columns.
+#include <math.h>
+#include <type_traits>
+
+#include "common.h"
+
+namespace kda {
+namespace gemm {
+
+constexpr int kWavesM = 2, kWavesN = 4;     // wave grid of a workgroup
+constexpr int kWaves = kWavesM * kWavesN;     // 8 waves: 2 per SIMD
+constexpr int kThreads = 64 * kWaves;
+constexpr int kBK = 32;        // k per LDS slot
+constexpr int kStages = 4;     // LDS slots (4 x 32 KiB for a 256x256 tile)
+constexpr int kGroupM = 8;
+constexpr int kXcds = 8;
+constexpr int kMaxSeg = 6;
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+#define KDA_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+// 16 zero bytes: the DMA source for k-chunks past K (so they contribute 0).
+__device__ __align__(16) uint32_t g_zero_chunk[4] = {0u, 0u, 0u, 0u};
+
+enum class Epi {
+  kStore,          // bf16 C
+  kRowScale,       // bf16 C = acc * row_scale[m]
+  kSwiGLU,         // bf16 H = silu(acc_gate) * acc_up
+  kStoreF32,       // fp32 C
+  kSwiGLUF32,      // fp32 H = silu(acc_gate) * acc_up
+  kAddZSsqF32,     // fp32 C = acc + z; part[m][n/64] = sum over the 64 columns of C^2
+};
+
+// One K-segment: A_s (M x k), B_s (k x N) (and B2_s for two-B kernels).
+struct Seg {
+  const uint16_t* a;   // A_KMAJ: a[m*lda + k]; else a[k*lda + m]
+  const uint16_t* b;   // b[k*ldb + n]
+  const uint16_t* b2;  // b2[k*ldb + n]   (second B operand, SwiGLU)
+  int64_t lda, ldb;    // < 2^31
+  int k;               // k extent; a multiple of kBK unless it is the only segment
+};
+
+struct Params {
+  Seg seg[kMaxSeg];
+  int nseg;
+  void* c;                 // c[m*ldc + n]  (bf16, or fp32 for the *F32 epilogues)
+  const float* row_scale;  // [M]                      (kRowScale)
+  const float* z;          // z[m*ldc + n], fp32       (kAddZSsqF32)
+  float* part;             // part[m*(N/64) + n/64]    (kAddZSsqF32)
+  int64_t ldc;
+  int64_t batch_a, batch_b, batch_c;   // per-batch strides (elements), batch = blockIdx.y
+  int m, n, k;             // k = sum of segment extents
+};
+
+// Position of 16-byte chunk c of row r in a K-contiguous tile of BK-element
+// rows: 64-byte rows (BK=32, 4 chunks) or 128-byte rows (BK=64, 8 chunks).
+// Both are measured conflict-free for the fragment read (16 consecutive rows,
+// one chunk) at the LDS's 256 B/clk ds_read_b128 rate.
+template <int BK>
+__device__ __forceinline__ int kswz(int r) { return BK == 32 ? ((r >> 1) & 3) : (r & 7); }
+// Position of 32-byte segment s of k-row k in an MN-contiguous tile (measured
+// conflict-free for the ds_read_b64_tr_b16 fragment read).
+__device__ __forceinline__ int mswz(int k) { return (k & 3) | (((k >> 3) & 1) << 2); }
+
+// Maps the linear workgroup id to (tile_m, tile_n): XCD-contiguous, grouped by rows.
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  int pid = blockIdx.x;
+  const int full = (total / kXcds) * kXcds;
+  if (pid < full) pid = (pid % kXcds) * (full / kXcds) + pid / kXcds;
+  const int per_group = kGroupM * tiles_n;
+  const int group = pid / per_group;
+  const int first_m = group * kGroupM;
+  const int gsize = min(tiles_m - first_m, kGroupM);
+  const int local = pid - group * per_group;
+  tm = first_m + local % gsize;
+  tn = local / gsize;
+}
+
+__device__ __forceinline__ float silu_f(float x) { return __fdividef(x, 1.0f + __expf(-x)); }
+
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2{lo, hi}), bf16x2));
+}
+
+// One 16-byte-per-lane DMA from global memory into LDS: lane i's 16 bytes at
+// `sbase + voff` land at LDS byte `lds + 16*i`.  The leading s_nop covers the
+// M0-write hazard.
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds) {
+  // the base is wave-uniform by construction; readfirstlane makes that visible
+  // (readfirstlane returns a signed int: widen through uint32_t, never sign-extend)
+  const uint64_t v = reinterpret_cast<uint64_t>(sbase);
+  const uint64_t u =
+      ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32)) << 32) |
+      (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff),
+               "s"(reinterpret_cast<const void*>(u)), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+// Same with a per-lane 64-bit address (used for the K tail, where lanes past K
+// read a zero chunk).
+__device__ __forceinline__ void dma16_ptr(const void* src, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)KDA_LDS_PTR(p);
+}
+
+// Reads the MFMA fragment (column `col0 + lane%16`, k = kbase + 8*(lane/16) .. +7)
+// of an MN-contiguous [BK][COLS] tile; col0 is a multiple of 16.
+template <int COLS>
+__device__ __forceinline__ bf16x8 read_mn_frag(const uint8_t* tile, int col0, int kbase, int lane) {
+  const int g = lane >> 4, jj = lane & 15;
+  const int s = col0 >> 4;
+  const int k0 = kbase + 8 * g + (jj >> 2);
+  const int k1 = k0 + 4;
+  const uint8_t* p0 = tile + k0 * (2 * COLS) + ((s ^ mswz(k0)) << 5) + 8 * (jj & 3);
+  const uint8_t* p1 = tile + k1 * (2 * COLS) + ((s ^ mswz(k1)) << 5) + 8 * (jj & 3);
+  const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16*)KDA_LDS_PTR(p0));
+  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16*)KDA_LDS_PTR(p1));
+  typedef short v8i16 __attribute__((ext_vector_type(8)));
+  const v8i16 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// Reads the MFMA fragment (row `row`, k = kbase + 8*(lane/16) .. +7) of a
+// K-contiguous [ROWS][BK] tile.
+template <int BK>
+__device__ __forceinline__ bf16x8 read_k_frag(const uint8_t* tile, int row, int kbase, int lane) {
+  const int c = (kbase >> 3) + (lane >> 4);
+  return *reinterpret_cast<const bf16x8*>(tile + row * (BK * 2) + ((c ^ kswz<BK>(row)) << 4));
+}
+
+template <int BM, int BN, int NB, bool A_KMAJ, Epi EPI, bool KTAIL, int BK, int STAGES, int NSEG>
+__global__ __launch_bounds__(kThreads, 1) void gemm_kernel(Params p) {
+  static_assert(NSEG >= 1 && NSEG <= kMaxSeg, "segments");
+  static_assert(NB == 1 || NB == 2, "one or two B operands");
+  static_assert(BM == 256 && BN % 128 == 0, "tile");
+  static_assert(STAGES >= 2, "ring depth");
+  static_assert(kWaves == 8, "ping-pong needs 8 waves");
+  constexpr int WM = BM / kWavesM, WN = BN / kWavesN;   // wave tile (per B operand)
+  constexpr int TM = WM / 16, TN = WN / 16;   // 16x16 MFMA tiles per wave
+  constexpr int NBF = NB * TN;                // B fragments per k-tile per wave
+  constexpr int A_BYTES = BM * BK * 2;
+  constexpr int B_BYTES = BN * BK * 2;        // per B operand
+  constexpr int STAGE = A_BYTES + NB * B_BYTES;
+  constexpr int A_INST = A_BYTES / 1024 / kWaves;  // DMA instructions per wave per slot
+  constexpr int B_INST = B_BYTES / 1024 / kWaves;  // ... per B operand
+  static_assert(A_INST >= 1 && B_INST >= 1, "DMA split");
+  constexpr int TILE_INST = A_INST + NB * B_INST;
+  constexpr int A_RPI = A_KMAJ ? 1024 / (2 * BK) : 1024 / (2 * BM);  // tile rows per DMA instruction
+  constexpr int B_RPI = 1024 / (2 * BN);
+  constexpr int A_LPR = 64 / A_RPI;           // lanes per tile row
+  constexpr int B_LPR = 64 / B_RPI;
+
+  extern __shared__ __align__(1024) uint8_t smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
+
+  const int tiles_m = (p.m + BM - 1) / BM, tiles_n = (p.n + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int M = p.m, N = p.n, K = p.k;
+  const int nk = (K + BK - 1) / BK;
+  const int64_t bz = blockIdx.y;
+
+  // ---- DMA sources.  Each lane keeps the (row, column) it fetches; its byte
+  // offset from the segment's per-batch base is formed per issue from the
+  // segment's leading dimension.  Rows/columns past M/N are clamped to the last
+  // valid one (their outputs are never stored).
+  int a_row[A_INST], a_col[A_INST], a_k[A_INST];   // a_k: k within the tile (K tail)
+#pragma unroll
+  for (int j = 0; j < A_INST; ++j) {
+    const int q = j * kWaves + wave;
+    const int r = q * A_RPI + lane / A_LPR;
+    const int t = lane % A_LPR;
+    if constexpr (A_KMAJ) {
+      const int c = t ^ kswz<BK>(r);
+      a_row[j] = min(m0 + r, M - 1);   // m
+      a_col[j] = 8 * c;                // k within the tile
+      a_k[j] = 8 * c;
+    } else {
+      const int s = (t >> 1) ^ mswz(r);
+      a_row[j] = r;                    // k within the tile
+      a_col[j] = min(m0 + s * 16 + (t & 1) * 8, M - 8);   // m
+      a_k[j] = r;
+    }
+  }
+  int b_row[B_INST], b_col[B_INST];
+#pragma unroll
+  for (int j = 0; j < B_INST; ++j) {
+    const int q = j * kWaves + wave;
+    const int r = q * B_RPI + lane / B_LPR;
+    const int t = lane % B_LPR;
+    const int s = (t >> 1) ^ mswz(r);
+    b_row[j] = r;
+    b_col[j] = min(n0 + s * 16 + (t & 1) * 8, N - 8);
+  }
+  const uint32_t lds0 = lds_addr(smem);
+
+  // Segment table, pinned in scalar registers (readfirstlane keeps the
+  // per-k-tile selection below a chain of scalar selects instead of an
+  // indexed load from a private copy of the kernel arguments).
+  auto rfl64 = [](const void* q) -> uint64_t {
+    const uint64_t v = reinterpret_cast<uint64_t>(q);
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32)) << 32) |
+           (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+  };
+  uint64_t seg_a[NSEG], seg_b[NSEG], seg_b2[NSEG];
+  uint32_t seg_lda[NSEG], seg_ldb[NSEG];
+  int seg_end[NSEG];   // first k-tile after the segment
+  {
+    int end = 0;
+#pragma unroll
+    for (int i = 0; i < NSEG; ++i) {
+      seg_a[i] = rfl64(p.seg[i].a);
+      seg_b[i] = rfl64(p.seg[i].b);
+      seg_b2[i] = NB == 2 ? rfl64(p.seg[i].b2) : 0;
+      seg_lda[i] = __builtin_amdgcn_readfirstlane((uint32_t)p.seg[i].lda);
+      seg_ldb[i] = __builtin_amdgcn_readfirstlane((uint32_t)p.seg[i].ldb);
+      end += (p.seg[i].k + BK - 1) / BK;
+      seg_end[i] = __builtin_amdgcn_readfirstlane(end);
+    }
+  }
+
+  // DMA of k-tile `kt` into ring slot `slot % STAGES`.
+  auto issue = [&](int kt, int slot) {
+    const uint32_t base = lds0 + (slot % STAGES) * STAGE;
+    uint64_t a64 = seg_a[0], b64 = seg_b[0], b264 = seg_b2[0];
+    uint32_t lda32 = seg_lda[0], ldb32 = seg_ldb[0];
+    int lt = kt;
+#pragma unroll
+    for (int i = 1; i < NSEG; ++i) {
+      const bool in = kt >= seg_end[i - 1];
+      a64 = in ? seg_a[i] : a64;
+      b64 = in ? seg_b[i] : b64;
+      b264 = in ? seg_b2[i] : b264;
+      lda32 = in ? seg_lda[i] : lda32;
+      ldb32 = in ? seg_ldb[i] : ldb32;
+      lt = in ? kt - seg_end[i - 1] : lt;
+    }
+    const uint16_t* a = reinterpret_cast<const uint16_t*>(a64);
+    const uint16_t* b = reinterpret_cast<const uint16_t*>(b64);
+    const uint16_t* b2 = reinterpret_cast<const uint16_t*>(b264);
+    const int64_t lda = lda32, ldb = ldb32;
+    const uint8_t* sa = reinterpret_cast<const uint8_t*>(a + bz * p.batch_a) +
+                        (A_KMAJ ? (int64_t)lt * BK * 2 : (int64_t)lt * BK * lda * 2);
+    const uint8_t* sb[NB];
+    sb[0] = reinterpret_cast<const uint8_t*>(b + bz * p.batch_b) + (int64_t)lt * BK * ldb * 2;
+    if constexpr (NB == 2)
+      sb[NB - 1] = reinterpret_cast<const uint8_t*>(b2 + bz * p.batch_b) + (int64_t)lt * BK * ldb * 2;
+    const bool tail = KTAIL && (kt + 1) * BK > K;
+    if (!tail) {
+#pragma unroll
+      for (int j = 0; j < A_INST; ++j)
+        dma16(sa, ((uint32_t)a_row[j] * lda32 + (uint32_t)a_col[j]) * 2u,
+              base + (j * kWaves + wave) * 1024);
+#pragma unroll
+      for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+        for (int j = 0; j < B_INST; ++j)
+          dma16(sb[bb], ((uint32_t)b_row[j] * ldb32 + (uint32_t)b_col[j]) * 2u,
+                base + A_BYTES + bb * B_BYTES + (j * kWaves + wave) * 1024);
+    } else {
+      const int kbase = kt * BK;
+#pragma unroll
+      for (int j = 0; j < A_INST; ++j) {
+        const void* src = (kbase + a_k[j] < K)
+                              ? (const void*)(sa + ((uint32_t)a_row[j] * lda32 + (uint32_t)a_col[j]) * 2u)
+                              : (const void*)g_zero_chunk;
+        dma16_ptr(src, base + (j * kWaves + wave) * 1024);
+      }
+#pragma unroll
+      for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+        for (int j = 0; j < B_INST; ++j) {
+          const void* src = (kbase + b_row[j] < K)
+                                ? (const void*)(sb[bb] + ((uint32_t)b_row[j] * ldb32 + (uint32_t)b_col[j]) * 2u)
+                                : (const void*)g_zero_chunk;
+          dma16_ptr(src, base + A_BYTES + bb * B_BYTES + (j * kWaves + wave) * 1024);
+        }
+    }
+  };
+
+  floatx4 acc[NB][TM][TN];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[b][i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  auto stage_ptr = [&](int kt) -> const uint8_t* { return smem + (kt % STAGES) * STAGE; };
+  auto read_a = [&](int kt, int kh, int i) -> bf16x8 {
+    const uint8_t* at = stage_ptr(kt);
+    if constexpr (A_KMAJ)
+      return read_k_frag<BK>(at, wm * WM + i * 16 + (lane & 15), kh * 32, lane);
+    else
+      return read_mn_frag<BM>(at, wm * WM + i * 16, kh * 32, lane);
+  };
+  auto read_b = [&](int kt, int kh, int bj) -> bf16x8 {
+    const int b = bj / TN, j = bj % TN;
+    return read_mn_frag<BN>(stage_ptr(kt) + A_BYTES + b * B_BYTES, wn * WN + j * 16, kh * 32, lane);
+  };
+
+  // ---- ping-pong schedule.  Waves 0-3 (group 0) and 4-7 (group 1) hold one
+  // wave per SIMD each and run the same program one phase apart: while one
+  // group issues the back-to-back MFMAs of a k-tile (raised priority), the
+  // other reads the fragments of its next k-tile from LDS.  One workgroup
+  // barrier per phase:
+  //   phase 2t:   group 0 loads tile t     group 1 computes tile t-1
+  //   phase 2t+1: group 0 computes tile t  group 1 loads tile t
+  // Tile t must be in LDS before phase 2t.  LEAD = how many k-tiles ahead the
+  // DMA runs:
+  //   * 2 (>= 3 slots): each wave issues its share of tile t while loading tile
+  //     t-2 (group 0: phase 2t-4, group 1: 2t-3) and awaits it at the end of
+  //     phase 2t-1 with only its share of tile t+1 in flight; the DMA of tile
+  //     t+2 overwrites the slot of tile t+2-STAGES, whose last reader (group 1)
+  //     finished in phase 2t+5-2*STAGES < 2t.
+  //   * 1 (2 slots): every wave issues its share of tile t+1 at the start of
+  //     phase 2t (group 0 while loading, group 1 while computing) into the slot
+  //     of tile t-1, last read in phase 2t-1, and awaits it at the end of 2t+1.
+  // Tile indices past the last k-tile are clamped: those DMAs re-read valid
+  // memory into slots that are no longer read.
+  constexpr int LEAD = STAGES >= 3 ? 2 : 1;
+  constexpr int KH = BK / 32;                   // 32-wide k halves per tile
+  const int grp = wave >> 2;
+  issue(0, 0);
+  if constexpr (LEAD == 2) {
+    issue(min(1, nk - 1), 1);
+    wait_vmcnt<TILE_INST>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  __builtin_amdgcn_s_barrier();
+  if (grp == 1) {
+    if constexpr (LEAD == 1) issue(min(1, nk - 1), 1);
+    __builtin_amdgcn_s_barrier();   // group 1 starts one phase later
+  }
+  asm volatile("" ::: "memory");
+
+  bf16x8 af[KH][TM], bfr[KH][NBF];
+  for (int kt = 0; kt < nk; ++kt) {
+    // -- load phase: fragments of tile kt
+    if (LEAD == 2 || grp == 0) issue(min(kt + LEAD, nk - 1), kt + LEAD);
+#pragma unroll
+    for (int kh = 0; kh < KH; ++kh) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[kh][i] = read_a(kt, kh, i);
+#pragma unroll
+      for (int bj = 0; bj < NBF; ++bj) bfr[kh][bj] = read_b(kt, kh, bj);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (grp == 1) {
+      if constexpr (LEAD == 2) wait_vmcnt<TILE_INST>();
+      else wait_vmcnt<0>();
+    }
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    // -- compute phase
+    if (LEAD == 1 && grp == 1 && kt + 2 <= nk) issue(min(kt + 2, nk - 1), kt + 2);
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int kh = 0; kh < KH; ++kh)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[b][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[kh][b * TN + j], af[kh][i],
+                                                                   acc[b][i][j], 0, 0, 0);
+    __builtin_amdgcn_s_setprio(0);
+    if (grp == 0) {
+      if constexpr (LEAD == 2) wait_vmcnt<TILE_INST>();
+      else wait_vmcnt<0>();
+    }
+    if (!(grp == 1 && kt + 1 == nk)) __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+  // No DMA may still be writing this workgroup's LDS when it exits.
+  wait_vmcnt<0>();
+
+  // ---- epilogue: lane holds C[row][col .. col+3] for each 16x16 tile
+  const int col_in = (lane >> 4) * 4;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int gm = m0 + wm * WM + i * 16 + (lane & 15);
+    const bool row_ok = gm < M;
+    float scale = 1.0f;
+    if constexpr (EPI == Epi::kRowScale) scale = row_ok ? p.row_scale[gm] : 0.f;
+    float ssq = 0.f;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int gn = n0 + wn * WN + j * 16 + col_in;
+      const bool ok = row_ok && gn < N;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if constexpr (EPI == Epi::kSwiGLU || EPI == Epi::kSwiGLUF32)
+          v[r] = silu_f(acc[0][i][j][r]) * acc[NB - 1][i][j][r];
+        else
+          v[r] = acc[0][i][j][r] * scale;
+      }
+      const int64_t off = bz * p.batch_c + (int64_t)gm * p.ldc + gn;
+      if constexpr (EPI == Epi::kAddZSsqF32) {
+        if (ok) {
+          const floatx4 zz = *reinterpret_cast<const floatx4*>(p.z + off);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            v[r] += zz[r];
+            ssq = fmaf(v[r], v[r], ssq);
+          }
+        }
+      }
+      if (!ok) continue;
+      if constexpr (EPI == Epi::kStoreF32 || EPI == Epi::kSwiGLUF32 || EPI == Epi::kAddZSsqF32) {
+        *reinterpret_cast<floatx4*>(reinterpret_cast<float*>(p.c) + off) =
+            floatx4{v[0], v[1], v[2], v[3]};
+      } else {
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.c) + off) =
+            u32x2{pack2(v[0], v[1]), pack2(v[2], v[3])};
+      }
+    }
+    if constexpr (EPI == Epi::kAddZSsqF32) {
+      // the 4 lanes l, l+16, l+32, l+48 hold the wave's 64 columns of this row
+      ssq += __shfl_xor(ssq, 16);
+      ssq += __shfl_xor(ssq, 32);
+      const int chunk = (n0 + wn * WN) / 64;
+      if (row_ok && lane < 16 && n0 + wn * WN < N)
+        p.part[(int64_t)gm * ((N + 63) / 64) + chunk] = ssq;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- pre-passes
+
+// fp32 -> (hi, lo) bf16 planes: hi = bf16(x), lo = bf16(x - hi), round to
+// nearest even.  Four elements per thread per step, grid-stride.
+__global__ __launch_bounds__(256) void split_f32_kernel(const floatx4* __restrict__ x,
+                                                        u32x2* __restrict__ hi, u32x2* __restrict__ lo,
+                                                        int64_t n4) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+    const floatx4 v = __builtin_nontemporal_load(x + i);
+    uint32_t h[4];
+    float l[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      h[e] = f32_to_bf16_bits(v[e]);
+      l[e] = v[e] - bf16_bits_to_f32(h[e]);
+    }
+    hi[i] = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    lo[i] = u32x2{f32_to_bf16_bits(l[0]) | (f32_to_bf16_bits(l[1]) << 16),
+                  f32_to_bf16_bits(l[2]) | (f32_to_bf16_bits(l[3]) << 16)};
+  }
+}
+
+// One workgroup per row of x [M][K] (fp32): y = x (+ z), then
+//   t = sum_k (y^2 / K) + eps;  y = y / sqrt(t) (* g)
+// in the reference's operation order, and the result is split into (hi, lo)
+// bf16 planes for the GEMM.  K % 4 == 0.
+constexpr int kRowThreads = 256;
+__global__ __launch_bounds__(kRowThreads) void rms_split_f32_kernel(
+    const float* __restrict__ x, const float* __restrict__ z, const float* __restrict__ g,
+    uint16_t* __restrict__ hi, uint16_t* __restrict__ lo, int k, float eps) {
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int k4 = k / 4;
+  const floatx4* xr = reinterpret_cast<const floatx4*>(x + (int64_t)row * k);
+  const floatx4* zr = z ? reinterpret_cast<const floatx4*>(z + (int64_t)row * k) : nullptr;
+  const float inv_k = 1.0f / (float)k;
+  float s = 0.f;
+  for (int c = tid; c < k4; c += kRowThreads) {
+    floatx4 v = xr[c];
+    if (zr) v += zr[c];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s += (v[e] * v[e]) * inv_k;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+  __shared__ float part[kRowThreads / 64];
+  if ((tid & 63) == 0) part[tid >> 6] = s;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < kRowThreads / 64; ++w) t += part[w];
+  const float rms = sqrtf(t + eps);
+  u32x2* hr = reinterpret_cast<u32x2*>(hi + (int64_t)row * k);
+  u32x2* lr = reinterpret_cast<u32x2*>(lo + (int64_t)row * k);
+  const floatx4* gr = reinterpret_cast<const floatx4*>(g);
+  for (int c = tid; c < k4; c += kRowThreads) {
+    floatx4 v = xr[c];
+    if (zr) v += zr[c];
+    uint32_t h[4];
+    float l[4];
+    const floatx4 gg = g ? gr[c] : floatx4{1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float y = (v[e] / rms) * gg[e];
+      h[e] = f32_to_bf16_bits(y);
+      l[e] = y - bf16_bits_to_f32(h[e]);
+    }
+    hr[c] = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    lr[c] = u32x2{f32_to_bf16_bits(l[0]) | (f32_to_bf16_bits(l[1]) << 16),
+                  f32_to_bf16_bits(l[2]) | (f32_to_bf16_bits(l[3]) << 16)};
+  }
+}
+
+// Row normalisation after a GEMM whose epilogue wrote y = x@w + z into `out` and
+// per-64-column sums of y^2 into part[M][ceil(N/64)]:
+//   out[m, n] = y[m, n] * g[n] / sqrt(sum_n y^2 / N + eps)
+__global__ __launch_bounds__(kRowThreads) void row_rmsnorm_f32_kernel(
+    float* __restrict__ out, const float* __restrict__ part, const float* __restrict__ g, int n,
+    float eps) {
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nchunk = (n + 63) / 64;
+  float s = 0.f;
+  for (int c = tid; c < nchunk; c += kRowThreads) s += part[(int64_t)row * nchunk + c];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+  __shared__ float wpart[kRowThreads / 64];
+  if ((tid & 63) == 0) wpart[tid >> 6] = s;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < kRowThreads / 64; ++w) t += wpart[w];
+  const float rms = sqrtf(t / (float)n + eps);
+  floatx4* orow = reinterpret_cast<floatx4*>(out + (int64_t)row * n);
+  const floatx4* gr = reinterpret_cast<const floatx4*>(g);
+  for (int c = tid; c < n / 4; c += kRowThreads) {
+    floatx4 v = orow[c];
+    const floatx4 gg = gr[c];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = v[e] * gg[e] / rms;
+    orow[c] = v;
+  }
+}
+
+// ---------------------------------------------------------------- RMSNorm pre-pass
+// One workgroup per row: inv_rms[m] = 1/sqrt(mean_k x[m,k]^2 + eps) (fp32 sum of
+// squares of the bf16 values) and xg[m,k] = bf16(x[m,k] * gamma[k]).  x is read
+// once; xg stays in the 256 MB Infinity Cache for the GEMM that follows.
+constexpr int kPrepThreads = 256;
+constexpr int kPrepVec = 4;   // 16-byte chunks per thread held in registers (K <= 8192)
+
+__global__ __launch_bounds__(kPrepThreads) void rms_prep_kernel(const uint16_t* __restrict__ x,
+                                                                const uint16_t* __restrict__ gamma,
+                                                                uint16_t* __restrict__ xg,
+                                                                float* __restrict__ inv_rms, int k,
+                                                                float eps) {
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nchunk = k / 8;
+  const u32x4* xr = reinterpret_cast<const u32x4*>(x + (int64_t)row * k);
+  u32x4 v[kPrepVec];
+  float ssq = 0.f;
+#pragma unroll
+  for (int u = 0; u < kPrepVec; ++u) {
+    const int c = tid + u * kPrepThreads;
+    v[u] = (c < nchunk) ? __builtin_nontemporal_load(xr + c) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float lo = __builtin_bit_cast(float, v[u][w] << 16);
+      const float hi = __builtin_bit_cast(float, v[u][w] & 0xffff0000u);
+      ssq = fmaf(lo, lo, ssq);
+      ssq = fmaf(hi, hi, ssq);
+    }
+  }
+  // tail chunks beyond the register-held part (K > 8192)
+  for (int c = tid + kPrepVec * kPrepThreads; c < nchunk; c += kPrepThreads) {
+    const u32x4 t = xr[c];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float lo = __builtin_bit_cast(float, t[w] << 16);
+      const float hi = __builtin_bit_cast(float, t[w] & 0xffff0000u);
+      ssq = fmaf(lo, lo, ssq);
+      ssq = fmaf(hi, hi, ssq);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ssq += __shfl_xor(ssq, off);
+  __shared__ float part[kPrepThreads / 64];
+  __shared__ float s_inv;
+  if ((tid & 63) == 0) part[tid >> 6] = ssq;
+  __syncthreads();
+  if (tid == 0) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < kPrepThreads / 64; ++w) s += part[w];
+    const float inv = 1.0f / sqrtf(s / (float)k + eps);
+    s_inv = inv;
+    inv_rms[row] = inv;
+  }
+  __syncthreads();
+  (void)s_inv;
+  const u32x4* gr = reinterpret_cast<const u32x4*>(gamma);
+  u32x4* outr = reinterpret_cast<u32x4*>(xg + (int64_t)row * k);
+  auto scale_store = [&](const u32x4& t, int c) {
+    const u32x4 g = gr[c];
+    u32x4 o;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float x0 = __builtin_bit_cast(float, t[w] << 16);
+      const float x1 = __builtin_bit_cast(float, t[w] & 0xffff0000u);
+      const float g0 = __builtin_bit_cast(float, g[w] << 16);
+      const float g1 = __builtin_bit_cast(float, g[w] & 0xffff0000u);
+      o[w] = pack2(x0 * g0, x1 * g1);
+    }
+    outr[c] = o;
+  };
+#pragma unroll
+  for (int u = 0; u < kPrepVec; ++u) {
+    const int c = tid + u * kPrepThreads;
+    if (c < nchunk) scale_store(v[u], c);
+  }
+  for (int c = tid + kPrepVec * kPrepThreads; c < nchunk; c += kPrepThreads) scale_store(xr[c], c);
+}
+
+
+// ---------------------------------------------------------------- launch helpers
+
+template <int BM, int BN, int NB, bool A_KMAJ, Epi EPI, int NSEG, int BK = kBK, int S = kStages>
+int launch_n(const Params& a, int batch, hipStream_t st, const char* what) {
+  const int tiles = ((a.m + BM - 1) / BM) * ((a.n + BN - 1) / BN);
+  const size_t lds = (size_t)S * (BM + NB * BN) * BK * sizeof(uint16_t);
+  static const bool attr_ok = [&] {
+    const hipError_t e1 = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(gemm_kernel<BM, BN, NB, A_KMAJ, EPI, false, BK, S, NSEG>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const hipError_t e2 = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(gemm_kernel<BM, BN, NB, A_KMAJ, EPI, true, BK, S, NSEG>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    return e1 == hipSuccess && e2 == hipSuccess;
+  }();
+  if (!attr_ok) return set_error(KDA_ERR_HIP, "%s: cannot reserve %zu bytes of LDS", what, lds);
+  if (batch > 65535) return set_error(KDA_ERR_UNSUPPORTED, "%s: batch %d too large", what, batch);
+  const dim3 grid(tiles, batch);
+  if (a.k % BK == 0)
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, NB, A_KMAJ, EPI, false, BK, S, NSEG>), grid, dim3(kThreads),
+                       lds, st, a);
+  else
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, NB, A_KMAJ, EPI, true, BK, S, NSEG>), grid, dim3(kThreads),
+                       lds, st, a);
+  return check_launch(what);
+}
+
+// Dispatches on the segment count (1, 3 or 6).
+template <int BM, int BN, int NB, bool A_KMAJ, Epi EPI>
+int launch(const Params& a, int batch, hipStream_t st, const char* what) {
+  switch (a.nseg) {
+    case 1: return launch_n<BM, BN, NB, A_KMAJ, EPI, 1>(a, batch, st, what);
+    case 3: return launch_n<BM, BN, NB, A_KMAJ, EPI, 3>(a, batch, st, what);
+    case 6: return launch_n<BM, BN, NB, A_KMAJ, EPI, 6>(a, batch, st, what);
+  }
+  return set_error(KDA_ERR_UNSUPPORTED, "%s: %d K-segments", what, a.nseg);
+}
+
+// Chooses the N tile: 256 when that still gives at least one wave of tiles over
+// the device, else 128 (more, smaller tiles for skinny problems).
+template <bool A_KMAJ, Epi EPI>
+int launch_auto(const Params& a, int batch, hipStream_t st, const char* what) {
+  const int64_t tiles256 = (int64_t)((a.m + 255) / 256) * ((a.n + 255) / 256) * batch;
+  if (tiles256 >= device_cu_count()) return launch<256, 256, 1, A_KMAJ, EPI>(a, batch, st, what);
+  return launch<256, 128, 1, A_KMAJ, EPI>(a, batch, st, what);
+}
+
+Params make_params(int64_t m, int64_t n, void* c, int64_t ldc) {
+  Params p{};
+  p.m = (int)m;
+  p.n = (int)n;
+  p.c = c;
+  p.ldc = ldc;
+  return p;
+}
+
+void add_seg(Params& p, const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t k,
+             const uint16_t* b2 = nullptr) {
+  Seg& s = p.seg[p.nseg++];
+  s.a = a;
+  s.b = b;
+  s.b2 = b2;
+  s.lda = lda;
+  s.ldb = ldb;
+  s.k = (int)k;
+  p.k += (int)k;
+}
+
+// The three K-segments of a split fp32 product A@B ~= Ah@Bh + Ah@Bl + Al@Bh.
+void add_split_segs(Params& p, const uint16_t* ah, const uint16_t* al, int64_t lda,
+                    const uint16_t* bh, const uint16_t* bl, int64_t ldb, int64_t k,
+                    const uint16_t* b2h = nullptr, const uint16_t* b2l = nullptr) {
+  add_seg(p, ah, lda, bh, ldb, k, b2h);
+  add_seg(p, ah, lda, bl, ldb, k, b2l);
+  add_seg(p, al, lda, bh, ldb, k, b2h);
+}
+
+int validate(const char* what, const void* a, const void* b, const void* c, int64_t m,
+             int64_t n, int64_t k) {
+  if (m < 0 || n < 0 || k < 0)
+    return set_error(KDA_ERR_INVALID_ARG, "%s: negative size (M=%lld N=%lld K=%lld)", what,
+                     (long long)m, (long long)n, (long long)k);
+  if (m > (1 << 30) || n > (1 << 30) || k > (1 << 30))
+    return set_error(KDA_ERR_UNSUPPORTED, "%s: size too large", what);
+  // 32-bit byte offsets address each operand (per batch) from a scalar base.
+  if (m * k * 2 > (int64_t)0xffffffff || k * n * 2 > (int64_t)0xffffffff)
+    return set_error(KDA_ERR_UNSUPPORTED, "%s: an operand exceeds 4 GiB", what);
+  if ((k % 8) || (n % 8))
+    return set_error(KDA_ERR_UNSUPPORTED,
+                     "%s: K (%lld) and N (%lld) must be multiples of 8 (16-byte rows)", what,
+                     (long long)k, (long long)n);
+  if (m && n && (!a || !b || !c)) return set_error(KDA_ERR_INVALID_ARG, "%s: null pointer", what);
+  if (!aligned16(a) || !aligned16(b) || !aligned16(c))
+    return set_error(KDA_ERR_INVALID_ARG, "%s: pointers must be 16-byte aligned", what);
+  return KDA_OK;
+}
+
+// Bump allocator over the caller's workspace; with base == nullptr it only
+// measures, so the size query and the entry points share one layout.
+struct Carve {
+  uint8_t* base;
+  int64_t used = 0;
+  template <class T>
+  T* take(int64_t count) {
+    const int64_t off = (used + 255) & ~int64_t(255);
+    used = off + count * (int64_t)sizeof(T);
+    return base ? reinterpret_cast<T*>(base + off) : nullptr;
+  }
+};
+
+int check_ws(const char* what, const void* ws, int64_t ws_bytes, int64_t need) {
+  if (need > 0 && (!ws || !aligned16(ws) || ws_bytes < need))
+    return set_error(KDA_ERR_INVALID_ARG,
+                     "%s: workspace must be 16-byte aligned and >= %lld bytes (got %lld)", what,
+                     (long long)need, (long long)ws_bytes);
+  return KDA_OK;
+}
+
+int split(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, hipStream_t st, const char* what) {
+  if (n % 4) return set_error(KDA_ERR_UNSUPPORTED, "%s: element count %lld not a multiple of 4", what, (long long)n);
+  if (!aligned16(x)) return set_error(KDA_ERR_INVALID_ARG, "%s: fp32 input must be 16-byte aligned", what);
+  const int64_t n4 = n / 4;
+  if (n4 == 0) return KDA_OK;
+  const int64_t blocks = std::min<int64_t>((n4 + 255) / 256, (int64_t)device_cu_count() * 16);
+  hipLaunchKernelGGL(split_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                     reinterpret_cast<const floatx4*>(x), reinterpret_cast<u32x2*>(hi),
+                     reinterpret_cast<u32x2*>(lo), n4);
+  return check_launch(what);
+}
+
+// ---- workspace plans (shared by the size query and the entry points)
+struct SplitPlan {     // hi/lo planes of A [count_a] and B [count_b]
+  uint16_t *ah, *al, *bh, *bl;
+};
+SplitPlan plan_split(Carve& c, int64_t count_a, int64_t count_b) {
+  SplitPlan s;
+  s.ah = c.take<uint16_t>(count_a);
+  s.al = c.take<uint16_t>(count_a);
+  s.bh = c.take<uint16_t>(count_b);
+  s.bl = c.take<uint16_t>(count_b);
+  return s;
+}
+struct LoraPlan {
+  SplitPlan xw;        // x [M,K], w [K,N]
+  uint16_t *ah, *al;   // a [K,R]
+  float* t;            // x@a [M,R]
+  uint16_t *th, *tl;   // split t
+  uint16_t *bh, *bl;   // b [R,N]
+};
+LoraPlan plan_lora(Carve& c, int64_t m, int64_t k, int64_t n, int64_t r) {
+  LoraPlan p;
+  p.xw = plan_split(c, m * k, k * n);
+  p.ah = c.take<uint16_t>(k * r);
+  p.al = c.take<uint16_t>(k * r);
+  p.t = c.take<float>(m * r);
+  p.th = c.take<uint16_t>(m * r);
+  p.tl = c.take<uint16_t>(m * r);
+  p.bh = c.take<uint16_t>(r * n);
+  p.bl = c.take<uint16_t>(r * n);
+  return p;
+}
+struct SwigluPlan {
+  uint16_t *xh, *xl, *gh, *gl, *uh, *ul;
+  float* h;
+  uint16_t *hh, *hl, *dh, *dl;
+};
+SwigluPlan plan_swiglu(Carve& c, int64_t m, int64_t k, int64_t f) {
+  SwigluPlan p;
+  p.xh = c.take<uint16_t>(m * k);
+  p.xl = c.take<uint16_t>(m * k);
+  p.gh = c.take<uint16_t>(k * f);
+  p.gl = c.take<uint16_t>(k * f);
+  p.uh = c.take<uint16_t>(k * f);
+  p.ul = c.take<uint16_t>(k * f);
+  p.h = c.take<float>(m * f);
+  p.hh = c.take<uint16_t>(m * f);
+  p.hl = c.take<uint16_t>(m * f);
+  p.dh = c.take<uint16_t>(f * k);
+  p.dl = c.take<uint16_t>(f * k);
+  return p;
+}
+struct RmsBf16Plan {
+  uint16_t* xg;
+  float* inv;
+};
+RmsBf16Plan plan_rms_bf16(Carve& c, int64_t m, int64_t k) {
+  RmsBf16Plan p;
+  p.xg = c.take<uint16_t>(m * k);
+  p.inv = c.take<float>(m);
+  return p;
+}
+
+int64_t workspace_bytes(int op, int64_t b, int64_t m, int64_t k, int64_t n, int64_t r) {
+  Carve c{nullptr};
+  switch (op) {
+    case KDA_OP_MATMUL_F32:
+    case KDA_OP_TRANSPOSE_MATMUL_F32:
+    case KDA_OP_RMSNORM_MATMUL_F32:
+    case KDA_OP_ADD_RMSNORM_MATMUL_F32:
+      plan_split(c, m * k, k * n);
+      break;
+    case KDA_OP_MATMUL_ADD_RMSNORM_F32:
+      plan_split(c, m * k, k * n);
+      c.take<float>(m * ((n + 63) / 64));
+      break;
+    case KDA_OP_BMM_F32:
+      plan_split(c, b * m * k, b * k * n);
+      break;
+    case KDA_OP_LORA_F32:
+      plan_lora(c, m, k, n, r);
+      break;
+    case KDA_OP_SWIGLU_F32:
+      plan_swiglu(c, m, k, n);
+      break;
+    case KDA_OP_RMSNORM_MATMUL_BF16:
+      plan_rms_bf16(c, m, k);
+      break;
+    default:
+      return -1;
+  }
+  return c.used;
+}
+
+int check_split_k(const char* what, int64_t k) {
+  if (k % kBK)
+    return set_error(KDA_ERR_UNSUPPORTED, "%s: K (%lld) must be a multiple of %d on the fp32 path",
+                     what, (long long)k, kBK);
+  return KDA_OK;
+}
+
+}  // namespace gemm
+}  // namespace kda
+
+using namespace kda;
+using namespace kda::gemm;
+
+extern "C" int64_t kda_workspace_size(int op, int64_t batch, int64_t m, int64_t k, int64_t n,
+                                      int64_t r) {
+  if (batch < 0 || m < 0 || k < 0 || n < 0 || r < 0) return -1;
+  return workspace_bytes(op, batch, m, k, n, r);
+}
+
+// ---------------------------------------------------------------- bf16 entry points
+
+extern "C" int kda_matmul_bf16(const kda_bf16* a, const kda_bf16* b, kda_bf16* c, int64_t m,
+                               int64_t k, int64_t n, void* stream) {
+  clear_error();
+  if (int rc = validate("matmul_bf16", a, b, c, m, n, k)) return rc;
+  if (m == 0 || n == 0) return KDA_OK;
+  if (k == 0) return hipMemsetAsync(c, 0, (size_t)m * n * 2, as_stream(stream)) == hipSuccess
+                         ? KDA_OK : set_error(KDA_ERR_HIP, "matmul_bf16: memset failed");
+  Params p = make_params(m, n, c, n);
+  add_seg(p, a, k, b, n, k);
+  return launch_auto<true, Epi::kStore>(p, 1, as_stream(stream), "matmul_bf16");
+}
+
+extern "C" int kda_rmsnorm_matmul_bf16(const kda_bf16* x, const kda_bf16* gamma, const kda_bf16* w,
+                                       kda_bf16* y, int64_t m, int64_t k, int64_t n, float eps,
+                                       void* workspace, int64_t workspace_bytes_, void* stream) {
+  clear_error();
+  const char* what = "rmsnorm_matmul_bf16";
+  if (int rc = validate(what, x, w, y, m, n, k)) return rc;
+  if (k == 0) return set_error(KDA_ERR_INVALID_ARG, "%s: K must be > 0", what);
+  if (!gamma || !aligned16(gamma))
+    return set_error(KDA_ERR_INVALID_ARG, "%s: gamma null or not 16-byte aligned", what);
+  if (!(eps >= 0.f)) return set_error(KDA_ERR_INVALID_ARG, "%s: eps must be >= 0", what);
+  if (m == 0 || n == 0) return KDA_OK;
+  if (int rc = check_ws(what, workspace, workspace_bytes_,
+                        workspace_bytes(KDA_OP_RMSNORM_MATMUL_BF16, 1, m, k, n, 0)))
+    return rc;
+  Carve cv{reinterpret_cast<uint8_t*>(workspace)};
+  const RmsBf16Plan wp = plan_rms_bf16(cv, m, k);
+  hipStream_t st = as_stream(stream);
+  hipLaunchKernelGGL(rms_prep_kernel, dim3((unsigned)m), dim3(kPrepThreads), 0, st, x, gamma, wp.xg,
+                     wp.inv, (int)k, eps);
+  if (int rc = check_launch("rmsnorm_matmul_bf16(prep)")) return rc;
+  Params p = make_params(m, n, y, n);
+  p.row_scale = wp.inv;
+  add_seg(p, wp.xg, k, w, n, k);
+  return launch_auto<true, Epi::kRowScale>(p, 1, st, what);
+}
+
+extern "C" int kda_swiglu_bf16(const kda_bf16* x, const kda_bf16* w_up, const kda_bf16* w_down,
+                               const kda_bf16* w_gate, kda_bf16* h, kda_bf16* y, int64_t m,
+                               int64_t k, int64_t f, void* stream) {
+  clear_error();
+  if (int rc = validate("swiglu_bf16(up/gate)", x, w_gate, h, m, f, k)) return rc;
+  if (int rc = validate("swiglu_bf16(down)", h, w_down, y, m, k, f)) return rc;
+  if (!w_up || !aligned16(w_up))
+    return set_error(KDA_ERR_INVALID_ARG, "swiglu_bf16: w_up null or misaligned");
+  if (m == 0 || k == 0) return KDA_OK;
+  if (f == 0) return hipMemsetAsync(y, 0, (size_t)m * k * 2, as_stream(stream)) == hipSuccess
+                         ? KDA_OK : set_error(KDA_ERR_HIP, "swiglu_bf16: memset failed");
+  hipStream_t st = as_stream(stream);
+  Params up = make_params(m, f, h, f);
+  add_seg(up, x, k, w_gate, f, k, w_up);
+  if (int rc = launch<256, 128, 2, true, Epi::kSwiGLU>(up, 1, st, "swiglu_bf16(up/gate)")) return rc;
+  Params down = make_params(m, k, y, k);
+  add_seg(down, h, f, w_down, k, f);
+  return launch_auto<true, Epi::kStore>(down, 1, st, "swiglu_bf16(down)");
+}
+
+// ---------------------------------------------------------------- fp32 entry points
+// fp32 operands, fp32 output, via the three-product bf16 split (see the header).
+
+extern "C" int kda_matmul_f32(const float* lhs, const float* rhs, float* out, int64_t m, int64_t k,
+                              int64_t n, void* workspace, int64_t ws_bytes, void* stream) {
+  clear_error();
+  const char* what = "matmul_f32";
+  if (int rc = validate(what, lhs, rhs, out, m, n, k)) return rc;
+  if (int rc = check_split_k(what, k)) return rc;
+  if (m == 0 || n == 0) return KDA_OK;
+  if (k == 0) return hipMemsetAsync(out, 0, (size_t)m * n * 4, as_stream(stream)) == hipSuccess
+                         ? KDA_OK : set_error(KDA_ERR_HIP, "%s: memset failed", what);
+  if (int rc = check_ws(what, workspace, ws_bytes, workspace_bytes(KDA_OP_MATMUL_F32, 1, m, k, n, 0)))
+    return rc;
+  hipStream_t st = as_stream(stream);
+  Carve cv{reinterpret_cast<uint8_t*>(workspace)};
+  const SplitPlan s = plan_split(cv, m * k, k * n);
+  if (int rc = split(lhs, m * k, s.ah, s.al, st, what)) return rc;
+  if (int rc = split(rhs, k * n, s.bh, s.bl, st, what)) return rc;
+  Params p = make_params(m, n, out, n);
+  add_split_segs(p, s.ah, s.al, k, s.bh, s.bl, n, k);
+  return launch_auto<true, Epi::kStoreF32>(p, 1, st, what);
+}
+
+extern "C" int kda_transpose_matmul_f32(const float* lhs, const float* rhs, float* out, int64_t m,
+                                        int64_t k, int64_t n, void* workspace, int64_t ws_bytes,
+                                        void* stream) {
+  clear_error();
+  const char* what = "transpose_matmul_f32";
+  if (int rc = validate(what, lhs, rhs, out, m, n, k)) return rc;
+  if (int rc = check_split_k(what, k)) return rc;
+  if (m % 8) return set_error(KDA_ERR_UNSUPPORTED, "%s: M (%lld) must be a multiple of 8", what, (long long)m);
+  if (m == 0 || n == 0) return KDA_OK;
+  if (k == 0) return hipMemsetAsync(out, 0, (size_t)m * n * 4, as_stream(stream)) == hipSuccess
+                         ? KDA_OK : set_error(KDA_ERR_HIP, "%s: memset failed", what);
+  if (int rc = check_ws(what, workspace, ws_bytes,
+                        workspace_bytes(KDA_OP_TRANSPOSE_MATMUL_F32, 1, m, k, n, 0)))
+    return rc;
+  hipStream_t st = as_stream(stream);
+  Carve cv{reinterpret_cast<uint8_t*>(workspace)};
+  const SplitPlan s = plan_split(cv, m * k, k * n);
+  if (int rc = split(lhs, m * k, s.ah, s.al, st, what)) return rc;
+  if (int rc = split(rhs, k * n, s.bh, s.bl, st, what)) return rc;
+  Params p = make_params(m, n, out, n);
+  add_split_segs(p, s.ah, s.al, m, s.bh, s.bl, n, k);   // A stored [K][M]: lda = M
+  return launch_auto<false, Epi::kStoreF32>(p, 1, st, what);
+}
+
+extern "C" int kda_bmm_f32(const float* lhs, const float* rhs, float* out, int64_t batch, int64_t m,
+                           int64_t k, int64_t n, void* workspace, int64_t ws_bytes, void* stream) {
+  clear_error();
+  const char* what = "bmm_f32";
+  if (batch < 0) return set_error(KDA_ERR_INVALID_ARG, "%s: batch < 0", what);
+  if (int rc = validate(what, lhs, rhs, out, m, n, k)) return rc;
+  if (int rc = check_split_k(what, k)) return rc;
+  if (batch == 0 || m == 0 || n == 0) return KDA_OK;
+  if (k == 0) return hipMemsetAsync(out, 0, (size_t)batch * m * n * 4, as_stream(stream)) == hipSuccess
+                         ? KDA_OK : set_error(KDA_ERR_HIP, "%s: memset failed", what);
+  if (int rc = check_ws(what, workspace, ws_bytes, workspace_bytes(KDA_OP_BMM_F32, batch, m, k, n, 0)))
+    return rc;
+  hipStream_t st = as_stream(stream);
+  Carve cv{reinterpret_cast<uint8_t*>(workspace)};
+  const SplitPlan s = plan_split(cv, batch * m * k, batch * k * n);
+  if (int rc = split(lhs, batch * m * k, s.ah, s.al, st, what)) return rc;
+  if (int rc = split(rhs, batch * k * n, s.bh, s.bl, st, what)) return rc;
+  Params p = make_params(m, n, out, n);
+  add_split_segs(p, s.ah, s.al, k, s.bh, s.bl, n, k);
+  p.batch_a = m * k;
+  p.batch_b = k * n;
+  p.batch_c = m * n;
+  return launch_auto<true, Epi::kStoreF32>(p, (int)batch, st, what);
+}
+
+extern "C" int kda_lora_f32(const float* x, const float* w, const float* a, const float* b,
+                            float* out, int64_t m, int64_t k, int64_t n, int64_t r, void* workspace,
+                            int64_t ws_bytes, void* stream) {
+  clear_error();
+  const char* what = "lora_f32";
+  if (int rc = validate(what, x, w, out, m, n, k)) return rc;
+  if (int rc = validate(what, x, a, out, m, r, k)) return rc;
+  if (int rc = check_split_k(what, k)) return rc;
+  if (int rc = check_split_k(what, r)) return rc;
+  if (!b || !aligned16(b)) return set_error(KDA_ERR_INVALID_ARG, "%s: b null or misaligned", what);
+  if (m == 0 || n == 0) return KDA_OK;
+  if (int rc = check_ws(what, workspace, ws_bytes, workspace_bytes(KDA_OP_LORA_F32, 1, m, k, n, r)))
+    return rc;
+  hipStream_t st = as_stream(stream);
+  Carve cv{reinterpret_cast<uint8_t*>(workspace)};
+  const LoraPlan lp = plan_lora(cv, m, k, n, r);
+  if (int rc = split(x, m * k, lp.xw.ah, lp.xw.al, st, what)) return rc;
+  if (int rc = split(w, k * n, lp.xw.bh, lp.xw.bl, st, what)) return rc;
+  if (r > 0) {
+    if (int rc = split(a, k * r, lp.ah, lp.al, st, what)) return rc;
+    if (int rc = split(b, r * n, lp.bh, lp.bl, st, what)) return rc;
+    // t = x @ a  [M, R]
+    Params pt = make_params(m, r, lp.t, r);
+    add_split_segs(pt, lp.xw.ah, lp.xw.al, k, lp.ah, lp.al, r, k);
+    if (int rc = launch_auto<true, Epi::kStoreF32>(pt, 1, st, "lora_f32(x@a)")) return rc;
+    if (int rc = split(lp.t, m * r, lp.th, lp.tl, st, what)) return rc;
+  }
+  // out = x @ w + t @ b in one accumulation
+  Params p = make_params(m, n, out, n);
+  add_split_segs(p, lp.xw.ah, lp.xw.al, k, lp.xw.bh, lp.xw.bl, n, k);
+  if (r > 0) add_split_segs(p, lp.th, lp.tl, r, lp.bh, lp.bl, n, r);
+  if (p.k == 0) return hipMemsetAsync(out, 0, (size_t)m * n * 4, st) == hipSuccess
+                           ? KDA_OK : set_error(KDA_ERR_HIP, "%s: memset failed", what);
+  return launch_auto<true, Epi::kStoreF32>(p, 1, st, what);
+}
+
+// Shared body of the NKIBench rmsnorm_matmul / add_rmsnorm_matmul forwards.
+static int rms_matmul_f32(const char* what, int op, const float* x, const float* z, const float* g,
+                          const float* w, float* out, int64_t m, int64_t k, int64_t n, float eps,
+                          void* workspace, int64_t ws_bytes, void* stream) {
+  if (int rc = validate(what, x, w, out, m, n, k)) return rc;
+  if (int rc = check_split_k(what, k)) return rc;
+  if (k == 0) return set_error(KDA_ERR_INVALID_ARG, "%s: K must be > 0", what);
+  if ((z && !aligned16(z)) || (g && !aligned16(g)))
+    return set_error(KDA_ERR_INVALID_ARG, "%s: z and g must be 16-byte aligned", what);
+  if (!(eps >= 0.f)) return set_error(KDA_ERR_INVALID_ARG, "%s: eps must be >= 0", what);
+  if (m == 0 || n == 0) return KDA_OK;
+  if (int rc = check_ws(what, workspace, ws_bytes, workspace_bytes(op, 1, m, k, n, 0))) return rc;
+  hipStream_t st = as_stream(stream);
+  Carve cv{reinterpret_cast<uint8_t*>(workspace)};
+  const SplitPlan s = plan_split(cv, m * k, k * n);
+  hipLaunchKernelGGL(rms_split_f32_kernel, dim3((unsigned)m), dim3(kRowThreads), 0, st, x, z, g,
+                     s.ah, s.al, (int)k, eps);
+  if (int rc = check_launch(what)) return rc;
+  if (int rc = split(w, k * n, s.bh, s.bl, st, what)) return rc;
+  Params p = make_params(m, n, out, n);
+  add_split_segs(p, s.ah, s.al, k, s.bh, s.bl, n, k);
+  return launch_auto<true, Epi::kStoreF32>(p, 1, st, what);
+}
+
+extern "C" int kda_rmsnorm_matmul_f32(const float* x, const float* w, float* out, int64_t m,
+                                      int64_t k, int64_t n, void* workspace, int64_t ws_bytes,
+                                      void* stream) {
+  clear_error();
+  return rms_matmul_f32("rmsnorm_matmul_f32", KDA_OP_RMSNORM_MATMUL_F32, x, nullptr, nullptr, w,
+                        out, m, k, n, 0.0f, workspace, ws_bytes, stream);
+}
+
+extern "C" int kda_add_rmsnorm_matmul_f32(const float* x, const float* w, float eps, const float* z,
+                                          const float* g, float* out, int64_t m, int64_t k,
+                                          int64_t n, void* workspace, int64_t ws_bytes,
+                                          void* stream) {
+  clear_error();
+  if (!z || !g) return set_error(KDA_ERR_INVALID_ARG, "add_rmsnorm_matmul_f32: null z or g");
+  return rms_matmul_f32("add_rmsnorm_matmul_f32", KDA_OP_ADD_RMSNORM_MATMUL_F32, x, z, g, w, out,
+                        m, k, n, eps, workspace, ws_bytes, stream);
+}
+
+extern "C" int kda_matmul_add_rmsnorm_f32(const float* x, const float* w, float eps, const float* z,
+                                          const float* g, float* out, int64_t m, int64_t k,
+                                          int64_t n, void* workspace, int64_t ws_bytes,
+                                          void* stream) {
+  clear_error();
+  const char* what = "matmul_add_rmsnorm_f32";
+  if (int rc = validate(what, x, w, out, m, n, k)) return rc;
+  if (int rc = check_split_k(what, k)) return rc;
+  if (!z || !g || !aligned16(z) || !aligned16(g))
+    return set_error(KDA_ERR_INVALID_ARG, "%s: z and g must be non-null and 16-byte aligned", what);
+  if (!(eps >= 0.f)) return set_error(KDA_ERR_INVALID_ARG, "%s: eps must be >= 0", what);
+  if (m == 0 || n == 0) return KDA_OK;
+  if (k == 0) return set_error(KDA_ERR_INVALID_ARG, "%s: K must be > 0", what);
+  if (int rc = check_ws(what, workspace, ws_bytes,
+                        workspace_bytes(KDA_OP_MATMUL_ADD_RMSNORM_F32, 1, m, k, n, 0)))
+    return rc;
+  hipStream_t st = as_stream(stream);
+  Carve cv{reinterpret_cast<uint8_t*>(workspace)};
+  const SplitPlan s = plan_split(cv, m * k, k * n);
+  float* part = cv.take<float>(m * ((n + 63) / 64));
+  if (int rc = split(x, m * k, s.ah, s.al, st, what)) return rc;
+  if (int rc = split(w, k * n, s.bh, s.bl, st, what)) return rc;
+  Params p = make_params(m, n, out, n);
+  add_split_segs(p, s.ah, s.al, k, s.bh, s.bl, n, k);
+  p.z = z;
+  p.part = part;
+  // the per-64-column row partials need 64-column wave tiles: 256-wide N tiles
+  if (int rc = launch<256, 256, 1, true, Epi::kAddZSsqF32>(p, 1, st, what)) return rc;
+  hipLaunchKernelGGL(row_rmsnorm_f32_kernel, dim3((unsigned)m), dim3(kRowThreads), 0, st, out,
+                     part, g, (int)n, eps);
+  return check_launch(what);
+}
+
+extern "C" int kda_swiglu_f32(const float* x, const float* w_up, const float* w_down,
+                              const float* w_gate, float* out, int64_t m, int64_t k, int64_t f,
+                              void* workspace, int64_t ws_bytes, void* stream) {
+  clear_error();
+  const char* what = "swiglu_f32";
+  if (int rc = validate(what, x, w_gate, out, m, f, k)) return rc;
+  if (int rc = validate(what, x, w_down, out, m, k, f)) return rc;
+  if (int rc = check_split_k(what, k)) return rc;
+  if (int rc = check_split_k(what, f)) return rc;
+  if (!w_up || !aligned16(w_up)) return set_error(KDA_ERR_INVALID_ARG, "%s: w_up null or misaligned", what);
+  if (m == 0 || k == 0) return KDA_OK;
+  if (f == 0) return hipMemsetAsync(out, 0, (size_t)m * k * 4, as_stream(stream)) == hipSuccess
+                         ? KDA_OK : set_error(KDA_ERR_HIP, "%s: memset failed", what);
+  if (int rc = check_ws(what, workspace, ws_bytes, workspace_bytes(KDA_OP_SWIGLU_F32, 1, m, k, f, 0)))
+    return rc;
+  hipStream_t st = as_stream(stream);
+  Carve cv{reinterpret_cast<uint8_t*>(workspace)};
+  const SwigluPlan sp = plan_swiglu(cv, m, k, f);
+  if (int rc = split(x, m * k, sp.xh, sp.xl, st, what)) return rc;
+  if (int rc = split(w_gate, k * f, sp.gh, sp.gl, st, what)) return rc;
+  if (int rc = split(w_up, k * f, sp.uh, sp.ul, st, what)) return rc;
+  Params up = make_params(m, f, sp.h, f);
+  add_split_segs(up, sp.xh, sp.xl, k, sp.gh, sp.gl, f, k, sp.uh, sp.ul);
+  if (int rc = launch<256, 128, 2, true, Epi::kSwiGLUF32>(up, 1, st, "swiglu_f32(up/gate)")) return rc;
+  if (int rc = split(sp.h, m * f, sp.hh, sp.hl, st, what)) return rc;
+  if (int rc = split(w_down, f * k, sp.dh, sp.dl, st, what)) return rc;
+  Params down = make_params(m, k, out, k);
+  add_split_segs(down, sp.hh, sp.hl, f, sp.dh, sp.dl, k, f);
+  return launch_auto<true, Epi::kStoreF32>(down, 1, st, "swiglu_f32(down)");
+}

@@ -30,7 +30,15 @@ SIGNATURES = {
     "kda_rope_f32": [_p, _p, _p, _p, _i64, _i64, _p],
     "kda_matmul_bf16": [_p, _p, _p, _i64, _i64, _i64, _p],
     "kda_rmsnorm_matmul_bf16": [_p, _p, _p, _p, _i64, _i64, _i64, _f32, _p, _i64, _p],
-    "kda_rmsnorm_matmul_bf16_workspace_size": [_i64, _i64],
+    "kda_workspace_size": [_int, _i64, _i64, _i64, _i64, _i64],
+    "kda_matmul_f32": [_p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
+    "kda_transpose_matmul_f32": [_p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
+    "kda_bmm_f32": [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p],
+    "kda_lora_f32": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p],
+    "kda_rmsnorm_matmul_f32": [_p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
+    "kda_add_rmsnorm_matmul_f32": [_p, _p, _f32, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
+    "kda_matmul_add_rmsnorm_f32": [_p, _p, _f32, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
+    "kda_swiglu_f32": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
     "kda_swiglu_bf16": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "kda_gqa_fwd_bf16": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _int,
                          _i64, _i64, _i64, _p],
@@ -39,8 +47,19 @@ SIGNATURES = {
 
 # Entry points that return something other than an int status.
 RESTYPES = {
-    "kda_rmsnorm_matmul_bf16_workspace_size": _i64,
+    "kda_workspace_size": _i64,
 }
+
+# Operator ids of kda_workspace_size (include/kda.h).
+OP_MATMUL_F32 = 1
+OP_TRANSPOSE_MATMUL_F32 = 2
+OP_BMM_F32 = 3
+OP_LORA_F32 = 4
+OP_RMSNORM_MATMUL_F32 = 5
+OP_ADD_RMSNORM_MATMUL_F32 = 6
+OP_MATMUL_ADD_RMSNORM_F32 = 7
+OP_SWIGLU_F32 = 8
+OP_RMSNORM_MATMUL_BF16 = 9
 
 
 class KdaError(RuntimeError):

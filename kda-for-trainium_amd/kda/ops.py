@@ -22,9 +22,15 @@ __all__ = [
     "adamw",
     "adamw_step_",
     "rope_single_freq_apply",
+    "workspace_size",
     "matmul",
+    "transpose_matmul",
+    "bmm",
+    "lora",
     "rmsnorm_matmul",
     "rmsnorm_matmul_workspace_size",
+    "add_rmsnorm_matmul",
+    "matmul_add_rmsnorm",
     "swiglu",
     "gqa",
 ]
@@ -144,6 +150,30 @@ def rope_single_freq_apply(x_in: torch.Tensor, cos: torch.Tensor, sin: torch.Ten
 
 
 # ----------------------------------------------------------------- GEMM family
+#
+# bf16 inputs run on bf16 MFMA with fp32 accumulation and return bf16.  fp32
+# inputs (the reference's NKIBench operators) run on bf16 MFMA through a
+# three-product split (x = hi + lo, A@B ~= Ah@Bh + Ah@Bl + Al@Bh, fp32
+# accumulation) and return fp32; their intermediates live in a workspace that
+# is allocated here unless the caller passes ``workspace`` (a uint8 GPU tensor of
+# at least ``workspace_size(...)`` bytes).
+
+def workspace_size(op: int, batch: int = 0, m: int = 0, k: int = 0, n: int = 0, r: int = 0) -> int:
+    """Workspace bytes of operator id `op` (kda._lib.OP_*) at the given sizes."""
+    size = _lib.query("kda_workspace_size", int(op), int(batch), int(m), int(k), int(n), int(r))
+    if size < 0:
+        raise ValueError(f"workspace_size: bad operator {op} or sizes")
+    return size
+
+
+def _workspace(workspace: Optional[torch.Tensor], need: int, device: torch.device) -> torch.Tensor:
+    if workspace is None:
+        return torch.empty(max(need, 16), dtype=torch.uint8, device=device)
+    _check("workspace", workspace, torch.uint8, ndim=1)
+    if workspace.device != device:
+        raise ValueError("workspace must be on the inputs' device")
+    return workspace
+
 
 def _gemm_dims(name_a: str, a: torch.Tensor, name_b: str, b: torch.Tensor):
     if a.dim() != 2 or b.dim() != 2:
@@ -153,65 +183,178 @@ def _gemm_dims(name_a: str, a: torch.Tensor, name_b: str, b: torch.Tensor):
     return a.shape[0], a.shape[1], b.shape[1]
 
 
-def matmul(lhs: torch.Tensor, rhs: torch.Tensor) -> torch.Tensor:
-    """out = lhs @ rhs, lhs (M, K), rhs (K, N).
+def _same_dtype(*named):
+    dt = named[0][1].dtype
+    for name, t in named:
+        _check(name, t, dt)
+    if dt not in (BF16, F32):
+        raise ValueError(f"unsupported dtype {dt} (bf16 or fp32)")
+    _same_device(*(t for _, t in named))
+    return dt
 
-    bf16 inputs: bf16 MFMA with fp32 accumulation, bf16 output.
-    Reference: workspaces/matmul/runs/matmul_v1.py:10-111, forward ``lhs @ rhs``.
+
+def matmul(lhs: torch.Tensor, rhs: torch.Tensor, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out = lhs @ rhs, lhs (M, K), rhs (K, N); bf16 -> bf16, fp32 -> fp32 (split).
+
+    Reference: workspaces/matmul/runs/matmul_v3_bf16_split.py:10-161, forward
+    ``lhs @ rhs`` (workspaces/matmul/runs/offline_bf16_split_sim.py:137-139).
     """
-    _check("lhs", lhs, lhs.dtype)
-    _check("rhs", rhs, lhs.dtype)
-    _same_device(lhs, rhs)
+    dt = _same_dtype(("lhs", lhs), ("rhs", rhs))
     m, k, n = _gemm_dims("lhs", lhs, "rhs", rhs)
-    if lhs.dtype != BF16:
-        raise ValueError(f"matmul: unsupported dtype {lhs.dtype}")
-    out = torch.empty((m, n), dtype=BF16, device=lhs.device)
-    _lib.call("kda_matmul_bf16", lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), m, k, n, _stream(lhs))
+    out = torch.empty((m, n), dtype=dt, device=lhs.device)
+    if dt == BF16:
+        _lib.call("kda_matmul_bf16", lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), m, k, n, _stream(lhs))
+        return out
+    ws = _workspace(workspace, workspace_size(_lib.OP_MATMUL_F32, 1, m, k, n), lhs.device)
+    _lib.call("kda_matmul_f32", lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), m, k, n,
+              ws.data_ptr(), ws.numel(), _stream(lhs))
+    return out
+
+
+def transpose_matmul(lhs: torch.Tensor, rhs: torch.Tensor,
+                     workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out = lhs.T @ rhs with lhs (K, M), rhs (K, N), fp32.
+
+    Reference: workspaces/transpose_matmul/runs/tmm_v3_mblk16_bf16_split.py:10-41,
+    forward ``transpose(lhs) @ rhs`` (workspaces/transpose_matmul/runs/offline_bf16_split_sim.py:101-104).
+    """
+    _same_dtype(("lhs", lhs), ("rhs", rhs))
+    _check("lhs", lhs, F32, ndim=2)
+    _check("rhs", rhs, F32, ndim=2)
+    k, m = lhs.shape
+    if rhs.shape[0] != k:
+        raise ValueError(f"transpose_matmul: lhs {tuple(lhs.shape)} and rhs {tuple(rhs.shape)} differ in K")
+    n = rhs.shape[1]
+    out = torch.empty((m, n), dtype=F32, device=lhs.device)
+    ws = _workspace(workspace, workspace_size(_lib.OP_TRANSPOSE_MATMUL_F32, 1, m, k, n), lhs.device)
+    _lib.call("kda_transpose_matmul_f32", lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), m, k, n,
+              ws.data_ptr(), ws.numel(), _stream(lhs))
+    return out
+
+
+def bmm(lhs: torch.Tensor, rhs: torch.Tensor, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out[b] = lhs[b] @ rhs[b], lhs (B, M, K), rhs (B, K, N), fp32.
+
+    Reference: workspaces/bmm/runs/bmm_v2.py:10-41 (forward per-batch lhs[b] @ rhs[b],
+    workspaces/bmm/docs/draft-phase1.md:3-5).
+    """
+    _same_dtype(("lhs", lhs), ("rhs", rhs))
+    _check("lhs", lhs, F32, ndim=3)
+    _check("rhs", rhs, F32, ndim=3)
+    bsz, m, k = lhs.shape
+    if rhs.shape[0] != bsz or rhs.shape[1] != k:
+        raise ValueError(f"bmm: lhs {tuple(lhs.shape)} and rhs {tuple(rhs.shape)} are incompatible")
+    n = rhs.shape[2]
+    out = torch.empty((bsz, m, n), dtype=F32, device=lhs.device)
+    ws = _workspace(workspace, workspace_size(_lib.OP_BMM_F32, bsz, m, k, n), lhs.device)
+    _lib.call("kda_bmm_f32", lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), bsz, m, k, n,
+              ws.data_ptr(), ws.numel(), _stream(lhs))
+    return out
+
+
+def lora(x: torch.Tensor, w: torch.Tensor, a: torch.Tensor, b: torch.Tensor,
+         workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out = x @ w + (x @ a) @ b, x (M, K), w (K, N), a (K, R), b (R, N), fp32.
+
+    Reference: workspaces/lora/runs/lora_v3_bf16_split.py:10-64, forward
+    workspaces/lora/runs/offline_lora_bf16_split_sim.py:175-180.  Both terms
+    accumulate in one GEMM (six K-segments).
+    """
+    _same_dtype(("x", x), ("w", w), ("a", a), ("b", b))
+    for name, t in (("x", x), ("w", w), ("a", a), ("b", b)):
+        _check(name, t, F32, ndim=2)
+    m, k, n = _gemm_dims("x", x, "w", w)
+    r = a.shape[1]
+    if tuple(a.shape) != (k, r) or tuple(b.shape) != (r, n):
+        raise ValueError(f"lora: a must be {(k, r)} and b {(r, n)}, got {tuple(a.shape)}, {tuple(b.shape)}")
+    out = torch.empty((m, n), dtype=F32, device=x.device)
+    ws = _workspace(workspace, workspace_size(_lib.OP_LORA_F32, 1, m, k, n, r), x.device)
+    _lib.call("kda_lora_f32", x.data_ptr(), w.data_ptr(), a.data_ptr(), b.data_ptr(), out.data_ptr(),
+              m, k, n, r, ws.data_ptr(), ws.numel(), _stream(x))
     return out
 
 
 def rmsnorm_matmul(x: torch.Tensor, w: torch.Tensor, gamma: Optional[torch.Tensor] = None,
                    eps: float = 0.0, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """out = (x * rsqrt(mean_k(x^2) + eps) * gamma) @ w.
+    """out = (x * rsqrt(mean_k(x^2) + eps) * gamma) @ w, x (M, K), w (K, N).
 
-    x (M, K), w (K, N), gamma (K,) or None (no gain).  bf16 inputs: bf16 output,
-    fp32 accumulation and fp32 norm statistics.  A streaming pre-pass writes the
-    per-row 1/rms and bf16(x * gamma) into a workspace (``workspace``: a uint8
-    GPU tensor of at least ``rmsnorm_matmul_workspace_size(M, K)`` bytes, else
-    allocated here); the GEMM applies 1/rms in its epilogue.
-    Reference: workspaces/rmsnorm_matmul/runs/rmsnorm_matmul_v1.py:10-138
-    (forward x/sqrt(sum(x^2/K)) @ w: gamma=None, eps=0); with gain and eps as in
-    workspaces/add_rmsnorm_matmul/runs/offline_bf16_split_sim.py:97-106.
+    bf16: gamma (K,) or None; a streaming pre-pass writes the per-row 1/rms and
+    bf16(x * gamma), the GEMM applies 1/rms in its epilogue; bf16 output.
+    fp32: the NKIBench forward ``x / sqrt(sum(x^2 / K)) @ w`` (no gain, no eps;
+    gamma must be None and eps 0); fp32 output.
+    Reference: workspaces/rmsnorm_matmul/runs/rmsnorm_matmul_v1.py:10-138 (forward
+    workspaces/rmsnorm_matmul/runs/offline_bf16_split_sim.py:83-93); gain and eps
+    as in workspaces/add_rmsnorm_matmul/runs/offline_bf16_split_sim.py:97-106.
     """
-    _check("x", x, x.dtype)
-    _check("w", w, x.dtype)
-    _same_device(x, w)
+    dt = _same_dtype(("x", x), ("w", w))
     m, k, n = _gemm_dims("x", x, "w", w)
-    if x.dtype != BF16:
-        raise ValueError(f"rmsnorm_matmul: unsupported dtype {x.dtype}")
+    out = torch.empty((m, n), dtype=dt, device=x.device)
+    if dt == F32:
+        if gamma is not None or eps != 0.0:
+            raise ValueError("rmsnorm_matmul: the fp32 path is the NKIBench forward (no gamma, eps=0); "
+                             "use add_rmsnorm_matmul for gain and eps")
+        ws = _workspace(workspace, workspace_size(_lib.OP_RMSNORM_MATMUL_F32, 1, m, k, n), x.device)
+        _lib.call("kda_rmsnorm_matmul_f32", x.data_ptr(), w.data_ptr(), out.data_ptr(), m, k, n,
+                  ws.data_ptr(), ws.numel(), _stream(x))
+        return out
     if gamma is None:
         gamma = torch.ones(k, dtype=BF16, device=x.device)
     _check("gamma", gamma, BF16, shape=(k,))
     _same_device(x, gamma)
-    need = rmsnorm_matmul_workspace_size(m, k)
-    if workspace is None:
-        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=x.device)
-    _check("workspace", workspace, torch.uint8, ndim=1)
-    _same_device(x, workspace)
-    out = torch.empty((m, n), dtype=BF16, device=x.device)
+    ws = _workspace(workspace, workspace_size(_lib.OP_RMSNORM_MATMUL_BF16, 1, m, k, n), x.device)
     _lib.call("kda_rmsnorm_matmul_bf16", x.data_ptr(), gamma.data_ptr(), w.data_ptr(),
-              out.data_ptr(), m, k, n, float(eps), workspace.data_ptr(), workspace.numel(),
-              _stream(x))
+              out.data_ptr(), m, k, n, float(eps), ws.data_ptr(), ws.numel(), _stream(x))
     return out
 
 
 def rmsnorm_matmul_workspace_size(m: int, k: int) -> int:
-    """Bytes of workspace rmsnorm_matmul needs for an (m, k) x."""
-    return _lib.query("kda_rmsnorm_matmul_bf16_workspace_size", int(m), int(k))
+    """Bytes of workspace the bf16 rmsnorm_matmul needs for an (m, k) x."""
+    return workspace_size(_lib.OP_RMSNORM_MATMUL_BF16, 1, m, k, 0)
+
+
+def add_rmsnorm_matmul(x: torch.Tensor, w: torch.Tensor, eps: float, z: torch.Tensor,
+                       g: torch.Tensor, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = x + z; out = (y / sqrt(sum(y^2 / K) + eps) * g) @ w, fp32.
+
+    x, z (M, K), w (K, N), g (K,).  Argument order of forward(x, w, eps, z, g)
+    (workspaces/add_rmsnorm_matmul/docs/draft-phase1.md:10-24; kernel
+    workspaces/add_rmsnorm_matmul/runs/add_rmsnorm_matmul_v1.py:8-146).
+    """
+    _same_dtype(("x", x), ("w", w), ("z", z), ("g", g))
+    _check("x", x, F32, ndim=2)
+    m, k, n = _gemm_dims("x", x, "w", w)
+    _check("z", z, F32, shape=(m, k))
+    _check("g", g, F32, shape=(k,))
+    out = torch.empty((m, n), dtype=F32, device=x.device)
+    ws = _workspace(workspace, workspace_size(_lib.OP_ADD_RMSNORM_MATMUL_F32, 1, m, k, n), x.device)
+    _lib.call("kda_add_rmsnorm_matmul_f32", x.data_ptr(), w.data_ptr(), float(eps), z.data_ptr(),
+              g.data_ptr(), out.data_ptr(), m, k, n, ws.data_ptr(), ws.numel(), _stream(x))
+    return out
+
+
+def matmul_add_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, z: torch.Tensor,
+                       g: torch.Tensor, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = x @ w + z; out = y * g / sqrt(mean_n(y^2) + eps), fp32.
+
+    x (M, K), w (K, N), z (M, N), g (N,).  Argument order of forward(x, w, eps, z, g)
+    (workspaces/matmul_add_rmsnorm/docs/draft-phase1.md:10-22; kernel
+    workspaces/matmul_add_rmsnorm/runs/matmul_add_rmsnorm_v2_bf16_split.py:8-212).
+    """
+    _same_dtype(("x", x), ("w", w), ("z", z), ("g", g))
+    _check("x", x, F32, ndim=2)
+    m, k, n = _gemm_dims("x", x, "w", w)
+    _check("z", z, F32, shape=(m, n))
+    _check("g", g, F32, shape=(n,))
+    out = torch.empty((m, n), dtype=F32, device=x.device)
+    ws = _workspace(workspace, workspace_size(_lib.OP_MATMUL_ADD_RMSNORM_F32, 1, m, k, n), x.device)
+    _lib.call("kda_matmul_add_rmsnorm_f32", x.data_ptr(), w.data_ptr(), float(eps), z.data_ptr(),
+              g.data_ptr(), out.data_ptr(), m, k, n, ws.data_ptr(), ws.numel(), _stream(x))
+    return out
 
 
 def swiglu(x: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor, w_gate: torch.Tensor,
-           h_workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+           h_workspace: Optional[torch.Tensor] = None,
+           workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """out = (silu(x @ w_gate) * (x @ w_up)) @ w_down.
 
     x (M, K), w_up/w_gate (K, F), w_down (F, K); argument order of the reference
@@ -219,22 +362,25 @@ def swiglu(x: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor, w_gate: to
     kernel in workspaces/swiglu/runs/swiglu_v1.py:38-146).  bf16: the gated
     activation h (M, F) is produced by one fused dual-GEMM kernel (gate and up
     share each x tile; silu(gate)*up in the epilogue) and consumed by the down
-    GEMM.  ``h_workspace`` optionally supplies h's (M, F) bf16 buffer.
+    GEMM; ``h_workspace`` optionally supplies h's (M, F) bf16 buffer.  fp32: the
+    same two kernels on split operands, h in fp32 (``workspace``).
     """
-    _check("x", x, x.dtype)
+    dt = _same_dtype(("x", x), ("w_up", w_up), ("w_down", w_down), ("w_gate", w_gate))
     for name, t in (("w_up", w_up), ("w_down", w_down), ("w_gate", w_gate)):
-        _check(name, t, x.dtype, ndim=2)
-    _same_device(x, w_up, w_down, w_gate)
+        _check(name, t, dt, ndim=2)
     m, k, f = _gemm_dims("x", x, "w_up", w_up)
     if tuple(w_gate.shape) != (k, f) or tuple(w_down.shape) != (f, k):
         raise ValueError(f"swiglu: w_gate must be {(k, f)} and w_down {(f, k)}, got "
                          f"{tuple(w_gate.shape)}, {tuple(w_down.shape)}")
-    if x.dtype != BF16:
-        raise ValueError(f"swiglu: unsupported dtype {x.dtype}")
+    out = torch.empty((m, k), dtype=dt, device=x.device)
+    if dt == F32:
+        ws = _workspace(workspace, workspace_size(_lib.OP_SWIGLU_F32, 1, m, k, f), x.device)
+        _lib.call("kda_swiglu_f32", x.data_ptr(), w_up.data_ptr(), w_down.data_ptr(), w_gate.data_ptr(),
+                  out.data_ptr(), m, k, f, ws.data_ptr(), ws.numel(), _stream(x))
+        return out
     if h_workspace is None:
         h_workspace = torch.empty((m, f), dtype=BF16, device=x.device)
     _check("h_workspace", h_workspace, BF16, shape=(m, f))
-    out = torch.empty((m, k), dtype=BF16, device=x.device)
     _lib.call("kda_swiglu_bf16", x.data_ptr(), w_up.data_ptr(), w_down.data_ptr(), w_gate.data_ptr(),
               h_workspace.data_ptr(), out.data_ptr(), m, k, f, _stream(x))
     return out

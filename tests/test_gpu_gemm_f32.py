@@ -1,0 +1,112 @@
+"""GPU parity: the fp32 NKIBench GEMM operators (three-product bf16 split on MFMA)
+vs the fp32 numpy oracle.  Gate: relative-L2 <= 1e-5 (stricter than the
+reference's 2e-5, adapter/nkibench_case.py:51).
+
+Full NKIBench shapes on the five seeds (different inputs per seed), plus small
+and ragged shapes.  bmm's 1 GB output is compared on two sampled batches."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import SEEDS, to_dev, to_host
+from kda import ops
+from oracle import inputs as oi
+from oracle import ops as oo
+from oracle.numerics import rel_l2, split_bf16x2
+
+pytestmark = pytest.mark.gpu
+GATE = 1e-5
+
+
+def _run(case, fn, oracle_fn, seed, dims=None):
+    d = oi.draw(case, seed, dims=dims)
+    dev_in = {k: (to_dev(v, "cuda") if isinstance(v, np.ndarray) else v) for k, v in d.items()}
+    got = to_host(fn(**dev_in))
+    want = oracle_fn(**d)
+    err = rel_l2(got, want)
+    print(f"{case} seed={seed} dims={dims} rel_l2={err:.3e}", flush=True)
+    return err
+
+
+CASES = {
+    "matmul": (ops.matmul, oo.matmul),
+    "transpose_matmul": (ops.transpose_matmul, oo.transpose_matmul),
+    "lora": (ops.lora, oo.lora),
+    "rmsnorm_matmul": (ops.rmsnorm_matmul, oo.rmsnorm_matmul),
+    "add_rmsnorm_matmul": (ops.add_rmsnorm_matmul, oo.add_rmsnorm_matmul),
+    "matmul_add_rmsnorm": (ops.matmul_add_rmsnorm, oo.matmul_add_rmsnorm),
+    "swiglu": (ops.swiglu, oo.swiglu),
+}
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_full_size_all_seeds(case):
+    fn, ref = CASES[case]
+    for s in SEEDS:
+        assert _run(case, fn, ref, s) < GATE
+
+
+SMALL = {
+    "matmul": [dict(M=256, K=64, N=256), dict(M=37, K=96, N=40), dict(M=300, K=160, N=264),
+               dict(M=1, K=32, N=8)],
+    "transpose_matmul": [dict(M=256, K=64, N=256), dict(M=40, K=96, N=72), dict(M=264, K=160, N=136)],
+    "lora": [dict(M=256, K=64, N=256, R=32), dict(M=77, K=96, N=136, R=64)],
+    "rmsnorm_matmul": [dict(M=256, K=128, N=256), dict(M=50, K=96, N=72)],
+    "add_rmsnorm_matmul": [dict(M=256, K=128, N=256), dict(M=50, K=96, N=72)],
+    "matmul_add_rmsnorm": [dict(M=256, K=128, N=256), dict(M=50, K=96, N=200), dict(M=300, K=64, N=520)],
+    "swiglu": [dict(M=256, K=64, N=128), dict(M=50, K=96, N=160)],
+}
+
+
+@pytest.mark.parametrize("case,dims", [(c, d) for c, ds in SMALL.items() for d in ds])
+def test_small_and_ragged(case, dims):
+    fn, ref = CASES[case]
+    assert _run(case, fn, ref, 7, dims=dims) < GATE
+
+
+def test_bmm_full_size_sampled_batches():
+    for s in SEEDS:
+        d = oi.draw("bmm", s)
+        out = ops.bmm(to_dev(d["lhs"], "cuda"), to_dev(d["rhs"], "cuda"))
+        rng = np.random.default_rng(s)
+        picks = sorted({0, 15, int(rng.integers(16))})
+        got = to_host(out[picks])
+        want = oo.bmm(d["lhs"][picks], d["rhs"][picks])
+        err = rel_l2(got, want)
+        print(f"bmm seed={s} batches={picks} rel_l2={err:.3e}", flush=True)
+        assert err < GATE
+        del out
+        torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("dims", [dict(B=3, M=256, K=64, N=256), dict(B=2, M=100, K=96, N=72)])
+def test_bmm_small(dims):
+    assert _run("bmm", ops.bmm, oo.bmm, 5, dims=dims) < GATE
+
+
+def test_matmul_f32_layout_identity():
+    # A = I (hi = I, lo = 0) selects rows of B: the result is exactly hi(B) + lo(B),
+    # so any transposed or swizzled fragment, or a dropped split term, shows up exactly
+    k = 256
+    b = np.random.default_rng(0).standard_normal((k, 264)).astype(np.float32)
+    got = to_host(ops.matmul(to_dev(np.eye(k, dtype=np.float32), "cuda"), to_dev(b, "cuda")))
+    hi, lo = split_bf16x2(b)
+    np.testing.assert_array_equal(got, hi + lo)
+    assert rel_l2(got, b) < 1e-5
+
+
+def test_lora_rank_zero_term_matches_matmul():
+    # b = 0 removes the low-rank term: lora == matmul
+    d = oi.draw("lora", 3, dims=dict(M=256, K=128, N=256, R=32))
+    d["b"] = np.zeros_like(d["b"])
+    dev_in = {k: to_dev(v, "cuda") for k, v in d.items()}
+    a = to_host(ops.lora(**dev_in))
+    m = to_host(ops.matmul(dev_in["x"], dev_in["w"]))
+    np.testing.assert_array_equal(a, m)
+
+
+def test_fp32_path_rejects_unaligned_k():
+    x = torch.zeros(64, 40, device="cuda")
+    w = torch.zeros(40, 64, device="cuda")
+    with pytest.raises(ValueError, match="multiple of 32"):
+        ops.matmul(x, w)
