@@ -87,7 +87,8 @@ enum {
   KDA_OP_ADD_RMSNORM_MATMUL_F32 = 6,
   KDA_OP_MATMUL_ADD_RMSNORM_F32 = 7,
   KDA_OP_SWIGLU_F32 = 8,          /* n = F (intermediate width) */
-  KDA_OP_RMSNORM_MATMUL_BF16 = 9
+  KDA_OP_RMSNORM_MATMUL_BF16 = 9,
+  KDA_OP_BMM_SOFTMAX_F32 = 10
 };
 
 /* Workspace bytes for operator `op` at the given sizes (unused sizes: 0);
@@ -179,6 +180,18 @@ int kda_matmul_add_rmsnorm_f32(const float* x, const float* w, float eps, const 
 int kda_swiglu_f32(const float* x, const float* w_up, const float* w_down, const float* w_gate,
                    float* out, int64_t m, int64_t k, int64_t f, void* workspace,
                    int64_t workspace_bytes, void* stream);
+
+/* out[b, m, :] = softmax_n(lhs[b, m, :] @ rhs[b, :, :]) (max-shifted), fp32; lhs
+ * [B,M,K], rhs [B,K,N], out [B,M,N]; K <= 64, N a multiple of 64.  Scores on
+ * bf16 MFMA from a three-limb split of both operands (six products, residual
+ * ~2^-24: the softmax turns score errors into relative output errors); one
+ * fused kernel computes online row statistics, then recomputes the scores and
+ * writes the probabilities once.  Workspace: KDA_OP_BMM_SOFTMAX_F32.
+ * Replaces kernel(lhs, rhs) of workspaces/bmm_softmax/runs/bmm_softmax_v4.py:10-181
+ * (forward workspaces/bmm_softmax/docs/draft-phase1.md:14-23). */
+int kda_bmm_softmax_f32(const float* lhs, const float* rhs, float* out, int64_t batch, int64_t m,
+                        int64_t k, int64_t n, void* workspace, int64_t workspace_bytes,
+                        void* stream);
 
 /* ---------------------------------------------------------------- attention */
 

@@ -39,6 +39,7 @@ SIGNATURES = {
     "kda_add_rmsnorm_matmul_f32": [_p, _p, _f32, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
     "kda_matmul_add_rmsnorm_f32": [_p, _p, _f32, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
     "kda_swiglu_f32": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
+    "kda_bmm_softmax_f32": [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "kda_swiglu_bf16": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "kda_gqa_fwd_bf16": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _int,
                          _i64, _i64, _i64, _p],
@@ -60,6 +61,7 @@ OP_ADD_RMSNORM_MATMUL_F32 = 6
 OP_MATMUL_ADD_RMSNORM_F32 = 7
 OP_SWIGLU_F32 = 8
 OP_RMSNORM_MATMUL_BF16 = 9
+OP_BMM_SOFTMAX_F32 = 10
 
 
 class KdaError(RuntimeError):

@@ -26,6 +26,7 @@ __all__ = [
     "matmul",
     "transpose_matmul",
     "bmm",
+    "bmm_softmax",
     "lora",
     "rmsnorm_matmul",
     "rmsnorm_matmul_workspace_size",
@@ -248,6 +249,30 @@ def bmm(lhs: torch.Tensor, rhs: torch.Tensor, workspace: Optional[torch.Tensor] 
     out = torch.empty((bsz, m, n), dtype=F32, device=lhs.device)
     ws = _workspace(workspace, workspace_size(_lib.OP_BMM_F32, bsz, m, k, n), lhs.device)
     _lib.call("kda_bmm_f32", lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), bsz, m, k, n,
+              ws.data_ptr(), ws.numel(), _stream(lhs))
+    return out
+
+
+def bmm_softmax(lhs: torch.Tensor, rhs: torch.Tensor,
+                workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out = softmax(lhs @ rhs, axis=2) (max-shifted), lhs (B, M, K), rhs (B, K, N), fp32.
+
+    K <= 64, N a multiple of 64.  One fused kernel: online row statistics, then
+    the scores are recomputed and the probabilities written once.  Scores use a
+    three-limb bf16 split of both operands (six MFMA products).
+    Reference: workspaces/bmm_softmax/runs/bmm_softmax_v4.py:10-181, forward
+    workspaces/bmm_softmax/docs/draft-phase1.md:14-23.
+    """
+    _same_dtype(("lhs", lhs), ("rhs", rhs))
+    _check("lhs", lhs, F32, ndim=3)
+    _check("rhs", rhs, F32, ndim=3)
+    bsz, m, k = lhs.shape
+    if rhs.shape[0] != bsz or rhs.shape[1] != k:
+        raise ValueError(f"bmm_softmax: lhs {tuple(lhs.shape)} and rhs {tuple(rhs.shape)} are incompatible")
+    n = rhs.shape[2]
+    out = torch.empty((bsz, m, n), dtype=F32, device=lhs.device)
+    ws = _workspace(workspace, workspace_size(_lib.OP_BMM_SOFTMAX_F32, bsz, m, k, n), lhs.device)
+    _lib.call("kda_bmm_softmax_f32", lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), bsz, m, k, n,
               ws.data_ptr(), ws.numel(), _stream(lhs))
     return out
 
