@@ -193,6 +193,20 @@ int kda_bmm_softmax_f32(const float* lhs, const float* rhs, float* out, int64_t 
                         int64_t k, int64_t n, void* workspace, int64_t workspace_bytes,
                         void* stream);
 
+/* ---------------------------------------------------------------- selective scan */
+
+/* Mamba selective scan, fp32:
+ *   dA = exp(delta[c,m] * a[c,s]);  dBu = (delta[c,m] * b[s,m]) * u[c,m]
+ *   h[c,s,m] = dA * h[c,s,m-1] + dBu  (h = 0 before m = 0);  out[c,m] = sum_s c[s,m] h[c,s,m]
+ * delta, u, out [C,M]; a [C,S]; b, c [S,M]; 1 <= S <= 16.  Sequential over M per
+ * (channel, state) with numpy's rounding at every step (exp as numpy's float32 exp,
+ * pairwise sum over s): the result equals the numpy definition bit for bit.
+ * Replaces kernel(delta, u, a, b, c) of workspaces/mamba/runs/mamba_v4_s4unroll.py:7-117
+ * (forward workspaces/mamba/docs/draft-phase1.md:24-30). */
+int kda_mamba_f32(const float* delta, const float* u, const float* a, const float* b,
+                  const float* c, float* out, int64_t channels, int64_t seq, int64_t states,
+                  void* stream);
+
 /* ---------------------------------------------------------------- attention */
 
 /* Grouped-query softmax attention forward, bf16 in/out, fp32 online softmax:

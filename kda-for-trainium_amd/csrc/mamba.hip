@@ -1,0 +1,292 @@
+// Mamba selective scan, fp32 (NKIBench mamba), bit-identical to the numpy
+// definition it restates:
+//
+//   dA[c,s,m]  = exp(delta[c,m] * a[c,s])
+//   dBu[c,s,m] = (delta[c,m] * b[s,m]) * u[c,m]
+//   h[c,s,m]   = dA[c,s,m] * h[c,s,m-1] + dBu[c,s,m]        (h[c,s,-1] = 0)
+//   out[c,m]   = sum_s c[s,m] * h[c,s,m]
+//
+// delta, u [C, M]; a [C, S]; b, c [S, M]; out [C, M]; 1 <= S <= 16.
+//
+// Every rounding follows the numpy evaluation: separate multiply and add (no
+// contraction), exp evaluated as numpy's float32 SIMD exp evaluates it, and the
+// sum over s in numpy's pairwise order.  The recurrence runs sequentially over m
+// for each (c, s): any re-association of the scan (a chunked or tree scan) rounds
+// differently, and in fp32 those differences accumulate to a few 1e-6 relative
+// over a 7168-step sequence.
+//
+// Mapping: one workgroup per channel, 4 waves, the sequence in blocks of kT
+// steps, double-buffered in LDS.
+//   wave 0 (lanes 0..15, one per state) runs the recurrence over block k: two
+//     dependent VALU ops per step, operands read four steps at a time
+//     (ds_read_b128), states written back four steps at a time;
+//   waves 1..3 (192 lanes, one step each) meanwhile produce dA and dBu for block
+//     k+1 (coalesced loads of delta, u, b; 16 exps per lane) and reduce block k-1
+//     (h * c over s in numpy's order, one coalesced store of out per lane).
+// One barrier per block.  LDS rows are padded to kT+4 floats so the 16 state rows
+// read by wave 0 fall on distinct banks.
+#include <math.h>
+
+#include "common.h"
+
+namespace kda {
+namespace mamba {
+
+constexpr int kT = 192;            // steps per block (= producer lanes)
+constexpr int kRow = kT + 4;       // LDS row stride in floats
+constexpr int kMaxS = 16;
+constexpr int kThreads = 64 + kT;  // recurrence wave + producer waves
+
+struct Args {
+  const float* delta;  // [C][M]
+  const float* u;      // [C][M]
+  const float* a;      // [C][S]
+  const float* b;      // [S][M]
+  const float* c;      // [S][M]
+  float* out;          // [C][M]
+  int M, S, nb;
+};
+
+#pragma clang fp contract(off)
+
+// float32 exp evaluated the way numpy's SIMD loops evaluate np.exp on float32
+// (AVX2/FMA3 and AVX-512F share it; numpy/_core/src/umath/
+// loops_exponent_log.dispatch.c.src): k = rint(x*log2 e); Cody-Waite reduction
+// r = x - k ln2 with ln2 split in two parts (fused multiply-adds);
+// exp(r) = P5(r)/Q2(r), a rational minimax approximation evaluated by Horner with
+// fused multiply-adds and a correctly rounded division; result scaled by 2^k;
+// x >= 88.7228... gives inf, x <= -103.972... gives 0, NaN stays NaN.
+// Agrees bit for bit with np.exp on float32 over the sampled range [-104, 89].
+//
+// The division: r always lies in [-0.35, 0.35], so the numerator lies in
+// [0.70, 1.42] and the denominator in [0.90, 1.10].  For such operands the
+// general division (v_div_scale / v_div_fmas / v_div_fixup around a reciprocal
+// and three Newton/remainder steps) neither scales nor fixes up, so the core
+// sequence alone below gives the same correctly rounded quotient.
+__device__ __forceinline__ float np_expf(float x) {
+  const float kXmax = 0x1.62e43p+6f;    //  88.72283935546875
+  const float kXmin = -0x1.9fe36ap+6f;  // -103.97208404541015625
+  const float k = __builtin_rintf(x * 0x1.715476p+0f);  // log2(e); ties to even
+  float r = __builtin_fmaf(k, -0x1.62e4p-1f, x);
+  r = __builtin_fmaf(k, -0x1.7f7d1cp-20f, r);
+  float n = __builtin_fmaf(0x1.0a7bbp-11f, r, 0x1.bae2b2p-8f);
+  n = __builtin_fmaf(n, r, 0x1.a2fb18p-5f);
+  n = __builtin_fmaf(n, r, 0x1.fa98bp-3f);
+  n = __builtin_fmaf(n, r, 0x1.7397aap-1f);
+  n = __builtin_fmaf(n, r, 1.0f);
+  float d = __builtin_fmaf(0x1.61d064p-6f, r, -0x1.18d0aep-2f);
+  d = __builtin_fmaf(d, r, 1.0f);
+  float y = __builtin_amdgcn_rcpf(d);
+  y = __builtin_fmaf(__builtin_fmaf(-d, y, 1.0f), y, y);
+  float q = n * y;
+  q = __builtin_fmaf(__builtin_fmaf(-d, q, n), y, q);
+  q = __builtin_fmaf(__builtin_fmaf(-d, q, n), y, q);
+  float e = __builtin_ldexpf(q, (int)k);
+  e = (x >= kXmax) ? __builtin_inff() : e;
+  return (x <= kXmin) ? 0.f : e;
+}
+
+// numpy's pairwise summation of n <= 16 contiguous floats (the reduction loop of
+// np.add.reduce over a contiguous axis): n < 8 sequentially from 0; otherwise
+// eight partial sums (a[j] + a[j+8] when n == 16), combined as a balanced tree,
+// then the remaining a[8..n) added in order.
+__device__ __forceinline__ float np_pairwise_sum16(const float (&v)[kMaxS], int n) {
+  if (n < 8) {
+    float o = 0.f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      if (s < n) o += v[s];
+    return o;
+  }
+  float r[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = (n == 16) ? v[j] + v[j + 8] : v[j];
+  float o = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+  if (n < 16) {
+#pragma unroll
+    for (int s = 8; s < 16; ++s)
+      if (s < n) o += v[s];
+  }
+  return o;
+}
+
+struct Smem {
+  float da[2][kMaxS][kRow];
+  float dbu[2][kMaxS][kRow];
+  float h[2][kMaxS][kRow];
+};
+
+// Per-step inputs of one block, held in registers one block ahead of their use.
+struct StepIn {
+  float d, u, b[kMaxS];
+};
+
+__device__ __forceinline__ void load_step(StepIn& x, const Args& p, int64_t row, int t, int blk) {
+  const int m0 = blk * kT;
+  if (blk < p.nb && t < p.M - m0) {
+    x.d = p.delta[row + m0 + t];
+    x.u = p.u[row + m0 + t];
+#pragma unroll
+    for (int s = 0; s < kMaxS; ++s) x.b[s] = (s < p.S) ? p.b[(int64_t)s * p.M + m0 + t] : 0.f;
+  }
+}
+
+__device__ __forceinline__ void load_c(float (&cv)[kMaxS], const Args& p, int t, int blk) {
+  const int m0 = blk * kT;
+  if (t < p.M - m0) {
+#pragma unroll
+    for (int s = 0; s < kMaxS; ++s) cv[s] = (s < p.S) ? p.c[(int64_t)s * p.M + m0 + t] : 0.f;
+  }
+}
+
+// dA and dBu of step t of block `blk` into buffer `buf`; the padding steps up to
+// the next multiple of 16 get dA = 1, dBu = 0 (the recurrence passes h through
+// them unchanged); states s >= S get 0 (h stays 0).
+__device__ __forceinline__ void produce(Smem& sm, const Args& p, const StepIn& x,
+                                        const float (&av)[kMaxS], int t, int blk, int buf) {
+  const int len = min(kT, p.M - blk * kT);
+  if (t < len) {
+#pragma unroll
+    for (int s = 0; s < kMaxS; ++s) {
+      const float da = np_expf(x.d * av[s]);
+      const float dbu = (x.d * x.b[s]) * x.u;
+      sm.da[buf][s][t] = (s < p.S) ? da : 0.f;
+      sm.dbu[buf][s][t] = (s < p.S) ? dbu : 0.f;
+    }
+  } else if (t < ((len + 15) & ~15)) {
+#pragma unroll
+    for (int s = 0; s < kMaxS; ++s) {
+      sm.da[buf][s][t] = 1.f;
+      sm.dbu[buf][s][t] = 0.f;
+    }
+  }
+}
+
+// out[m0 + t] = sum_s h[s][t] * c[s][m0 + t] for the block in buffer `buf`
+__device__ __forceinline__ void reduce(const Smem& sm, const Args& p, const float (&cv)[kMaxS],
+                                       int64_t row, int t, int blk, int buf) {
+  const int m0 = blk * kT;
+  if (t >= min(kT, p.M - m0)) return;
+  float v[kMaxS];
+#pragma unroll
+  for (int s = 0; s < kMaxS; ++s) v[s] = (s < p.S) ? sm.h[buf][s][t] * cv[s] : 0.f;
+  p.out[row + m0 + t] = np_pairwise_sum16(v, p.S);
+}
+
+__global__ __launch_bounds__(kThreads) void scan_kernel(Args p) {
+  __shared__ __align__(16) Smem sm;
+  const int64_t row = (int64_t)blockIdx.x * p.M;
+  const int tid = threadIdx.x;
+  if (tid < 64) {
+    // recurrence wave: lane s carries h[c, s] through the whole sequence
+    const int s = tid;
+    float h = 0.f;
+    __syncthreads();  // block 0 produced
+    for (int k = 0; k < p.nb; ++k) {
+      const int buf = k & 1;
+      const int steps = (min(kT, p.M - k * kT) + 15) & ~15;
+      if (s < kMaxS) {
+        const float* pa = &sm.da[buf][s][0];
+        const float* pb = &sm.dbu[buf][s][0];
+        float* ph = &sm.h[buf][s][0];
+        // 16 steps per group; the next group's operands are read while this one runs
+        auto load = [&](float4 (&A)[4], float4 (&B)[4], int t) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            A[i] = *reinterpret_cast<const float4*>(pa + t + 4 * i);
+            B[i] = *reinterpret_cast<const float4*>(pb + t + 4 * i);
+          }
+        };
+        auto run = [&](const float4 (&A)[4], const float4 (&B)[4], int t) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float4 o;
+            h = A[i].x * h + B[i].x;
+            o.x = h;
+            h = A[i].y * h + B[i].y;
+            o.y = h;
+            h = A[i].z * h + B[i].z;
+            o.z = h;
+            h = A[i].w * h + B[i].w;
+            o.w = h;
+            *reinterpret_cast<float4*>(ph + t + 4 * i) = o;
+          }
+        };
+        float4 a0[4], b0[4], a1[4], b1[4];
+        load(a0, b0, 0);
+        for (int t = 0;; t += 32) {
+          const bool more1 = t + 16 < steps;
+          if (more1) load(a1, b1, t + 16);
+          run(a0, b0, t);
+          if (!more1) break;
+          const bool more2 = t + 32 < steps;
+          if (more2) load(a0, b0, t + 32);
+          run(a1, b1, t + 16);
+          if (!more2) break;
+        }
+      }
+      __syncthreads();  // block k consumed and its states written
+    }
+  } else {
+    const int t = tid - 64;
+    float av[kMaxS];
+#pragma unroll
+    for (int s = 0; s < kMaxS; ++s) av[s] = (s < p.S) ? p.a[(int64_t)blockIdx.x * p.S + s] : 0.f;
+    // Register prefetch: the inputs of block k+2 and c of block k are loaded in
+    // iteration k, one iteration before their use.
+    StepIn cur, nxt;
+    float c_use[kMaxS], c_nxt[kMaxS];
+    load_step(cur, p, row, t, 0);
+    load_step(nxt, p, row, t, 1);
+    produce(sm, p, cur, av, t, 0, 0);
+    __syncthreads();
+    for (int k = 0; k < p.nb; ++k) {
+      cur = nxt;  // block k+1
+      load_step(nxt, p, row, t, k + 2);
+#pragma unroll
+      for (int s = 0; s < kMaxS; ++s) c_use[s] = c_nxt[s];  // block k-1
+      load_c(c_nxt, p, t, k);
+      if (k + 1 < p.nb) produce(sm, p, cur, av, t, k + 1, (k + 1) & 1);
+      if (k >= 1) reduce(sm, p, c_use, row, t, k - 1, (k - 1) & 1);
+      __syncthreads();  // block k's states written by the recurrence wave
+    }
+    reduce(sm, p, c_nxt, row, t, p.nb - 1, (p.nb - 1) & 1);
+  }
+}
+
+#pragma clang fp contract(on)
+
+}  // namespace mamba
+}  // namespace kda
+
+using namespace kda;
+using namespace kda::mamba;
+
+extern "C" int kda_mamba_f32(const float* delta, const float* u, const float* a, const float* b,
+                             const float* c, float* out, int64_t channels, int64_t seq,
+                             int64_t states, void* stream) {
+  clear_error();
+  const char* what = "mamba_f32";
+  if (channels < 0 || seq < 0 || states < 0)
+    return set_error(KDA_ERR_INVALID_ARG, "%s: negative size", what);
+  if (states < 1 || states > kMaxS)
+    return set_error(KDA_ERR_UNSUPPORTED, "%s: states=%lld outside 1..%d", what, (long long)states,
+                     kMaxS);
+  if (channels > INT32_MAX || seq > INT32_MAX - kT)
+    return set_error(KDA_ERR_UNSUPPORTED, "%s: problem too large", what);
+  if (channels == 0 || seq == 0) return KDA_OK;
+  if (!delta || !u || !a || !b || !c || !out)
+    return set_error(KDA_ERR_INVALID_ARG, "%s: null pointer", what);
+  Args p;
+  p.delta = delta;
+  p.u = u;
+  p.a = a;
+  p.b = b;
+  p.c = c;
+  p.out = out;
+  p.M = (int)seq;
+  p.S = (int)states;
+  p.nb = (int)((seq + kT - 1) / kT);
+  hipLaunchKernelGGL(scan_kernel, dim3((unsigned)channels), dim3(kThreads), 0, as_stream(stream), p);
+  return check_launch(what);
+}

@@ -40,6 +40,7 @@ SIGNATURES = {
     "kda_matmul_add_rmsnorm_f32": [_p, _p, _f32, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
     "kda_swiglu_f32": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
     "kda_bmm_softmax_f32": [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p],
+    "kda_mamba_f32": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "kda_swiglu_bf16": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "kda_gqa_fwd_bf16": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _int,
                          _i64, _i64, _i64, _p],

@@ -33,6 +33,7 @@ __all__ = [
     "add_rmsnorm_matmul",
     "matmul_add_rmsnorm",
     "swiglu",
+    "mamba",
     "gqa",
 ]
 
@@ -408,6 +409,32 @@ def swiglu(x: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor, w_gate: to
     _check("h_workspace", h_workspace, BF16, shape=(m, f))
     _lib.call("kda_swiglu_bf16", x.data_ptr(), w_up.data_ptr(), w_down.data_ptr(), w_gate.data_ptr(),
               h_workspace.data_ptr(), out.data_ptr(), m, k, f, _stream(x))
+    return out
+
+
+# ----------------------------------------------------------------- selective scan
+
+def mamba(delta: torch.Tensor, u: torch.Tensor, a: torch.Tensor, b: torch.Tensor,
+          c: torch.Tensor) -> torch.Tensor:
+    """Selective scan, fp32: delta, u (C, M); a (C, S); b, c (S, M) -> out (C, M), S <= 16.
+
+    ``dA = exp(delta*a); dBu = delta*b*u; h = dA*h + dBu; out = sum_s c*h`` sequentially
+    over M (workspaces/mamba/docs/draft-phase1.md:24-30; kernel(delta, u, a, b, c) of
+    workspaces/mamba/runs/mamba_v4_s4unroll.py:7-117).  Every step rounds as numpy does
+    (numpy's float32 exp, pairwise sum over s), so the result equals the numpy definition.
+    """
+    for name, t in (("delta", delta), ("u", u), ("a", a), ("b", b), ("c", c)):
+        _check(name, t, F32, ndim=2)
+    _same_device(delta, u, a, b, c)
+    ch, m = delta.shape
+    s = a.shape[1]
+    if tuple(u.shape) != (ch, m) or tuple(a.shape) != (ch, s) or tuple(b.shape) != (s, m) \
+            or tuple(c.shape) != (s, m):
+        raise ValueError(f"mamba: inconsistent shapes delta {tuple(delta.shape)}, u {tuple(u.shape)}, "
+                         f"a {tuple(a.shape)}, b {tuple(b.shape)}, c {tuple(c.shape)}")
+    out = torch.empty((ch, m), dtype=F32, device=delta.device)
+    _lib.call("kda_mamba_f32", delta.data_ptr(), u.data_ptr(), a.data_ptr(), b.data_ptr(), c.data_ptr(),
+              out.data_ptr(), ch, m, s, _stream(delta))
     return out
 
 

@@ -1,0 +1,92 @@
+"""GPU parity: the Mamba selective scan vs the fp32 numpy oracle.
+
+The kernel rounds every step as the numpy definition does (numpy's float32 exp,
+no contraction, numpy's pairwise sum over the states), so the comparison is
+bit-exact; relative-L2 (the reference's gate is 3e-5 for this kernel,
+adapter/nkibench_case.py:53) is printed alongside.
+
+Full NKIBench shape (C=256, M=7168, S=16) on the five seeds, shapes that put the
+block boundaries, a ragged last block and every state count in play, and a direct
+check of the device exp against np.exp."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import SEEDS, to_dev, to_host
+from kda import ops
+from oracle import inputs as oi
+from oracle import ops as oo
+from oracle.numerics import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(d, label):
+    got = to_host(ops.mamba(**{k: to_dev(v, "cuda") for k, v in d.items()}))
+    want = oo.mamba(**d)
+    print(f"mamba {label} rel_l2={rel_l2(got, want):.3e} "
+          f"mismatches={int(np.count_nonzero(got != want))}", flush=True)
+    return got, want
+
+
+def test_full_size_all_seeds_bit_exact():
+    for s in SEEDS:
+        got, want = _run(oi.draw("mamba", s), f"seed={s}")
+        np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("dims", [
+    dict(C=4, M=192, S=16),       # exactly one block
+    dict(C=5, M=193, S=16),       # a one-step last block
+    dict(C=7, M=1000, S=5),       # ragged last block, S < 8
+    dict(C=3, M=31, S=1),         # single state, shorter than a 16-step group
+    dict(C=6, M=2049, S=12),      # 8 < S < 16: pairwise tree then sequential tail
+    dict(C=2, M=400, S=8),
+])
+def test_small_and_ragged_bit_exact(dims):
+    got, want = _run(oi.draw("mamba", 11, dims=dims), str(dims))
+    np.testing.assert_array_equal(got, want)
+
+
+def test_strong_decay_bit_exact():
+    # |delta*a| up to ~10: dA far from 1, exp over many binades
+    d = oi.draw("mamba", 2, dims=dict(C=8, M=1536, S=16))
+    d["delta"] = (np.abs(d["delta"]) * 40).astype(np.float32)
+    d["a"] = (-np.abs(d["a"]) * 40).astype(np.float32)
+    got, want = _run(d, "strong decay")
+    np.testing.assert_array_equal(got, want)
+
+
+def test_device_exp_matches_numpy():
+    # With M = 2, S = 1, a = 1, step 0 (delta = b = u = 1) sets h = 1 and step 1
+    # (delta = x, b = u = 0, c = 1) gives out[:, 1] = exp(x) * 1 + 0 = exp(x) exactly.
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.uniform(-103.9, 88.7, 120_000), rng.uniform(-0.4, 0.4, 120_000),
+        [0.0, -0.0, 1e-30, -1e-30, 0.34657359, -0.34657359, 88.72283, -103.97207, 80.0, -87.5,
+         -100.0],
+    ]).astype(np.float32)
+    n = x.size
+    ones = np.ones((n, 1), np.float32)
+    delta = np.concatenate([ones, x[:, None]], axis=1)
+    u = np.concatenate([ones, np.zeros((n, 1), np.float32)], axis=1)
+    b = np.array([[1.0, 0.0]], np.float32)
+    c = np.array([[1.0, 1.0]], np.float32)
+    out = to_host(ops.mamba(*(to_dev(t, "cuda") for t in (delta, u, ones, b, c))))
+    want = np.exp(x)
+    bad = np.nonzero(out[:, 1] != want)[0]
+    print(f"device exp: {bad.size} of {n} differ from np.exp", flush=True)
+    assert bad.size == 0, list(zip(x[bad[:5]], out[bad[:5], 1], want[bad[:5]]))
+
+
+def test_empty_and_rejections():
+    z = torch.zeros(4, 0, device="cuda")
+    a = torch.zeros(4, 8, device="cuda")
+    bc = torch.zeros(8, 0, device="cuda")
+    assert ops.mamba(z, z, a, bc, bc).shape == (4, 0)
+    d = torch.zeros(4, 32, device="cuda")
+    with pytest.raises(ValueError):  # S > 16
+        ops.mamba(d, d, torch.zeros(4, 17, device="cuda"), torch.zeros(17, 32, device="cuda"),
+                  torch.zeros(17, 32, device="cuda"))
+    with pytest.raises(ValueError):  # inconsistent b
+        ops.mamba(d, d, a, torch.zeros(8, 31, device="cuda"), torch.zeros(8, 32, device="cuda"))
