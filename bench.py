@@ -42,10 +42,11 @@ CONFIGS = {
                  work=2048 * 8192 * 8, kernels=["silu_vec_kernel"]),
     "rmsnorm_matmul": dict(desc="RMSNorm->matmul bf16 x[4096,4096] W[4096,11008]", dtype="bf16",
                            bound="mfma", work=2 * 4096 * 4096 * 11008,
-                           kernels=["rms_prep_kernel", "gemm_bf16_kernel<256,256,1,kRowScale>"]),
+                           kernels=["rms_prep_kernel", "gemm_kernel<256,256,1,A_KMAJ,Epi::kRowScale,...>"]),
     "swiglu": dict(desc="SwiGLU bf16 x[2048,4096] Wg/Wu[4096,14336] Wd[14336,4096]", dtype="bf16",
                    bound="mfma", work=6 * 2048 * 4096 * 14336,
-                   kernels=["gemm_bf16_kernel<256,128,2,kSwiGLU>", "gemm_bf16_kernel<256,128,1,kStore>"]),
+                   kernels=["gemm_kernel<256,128,2,A_KMAJ,Epi::kSwiGLU,...>",
+                            "gemm_kernel<256,128,1,A_KMAJ,Epi::kStore,...>"]),
     "adamw": dict(desc="AdamW fp32 n=2^27 in-place step 10", dtype="fp32", bound="hbm",
                   work=28 * (1 << 27), kernels=["adamw_vec_kernel<true>"]),
     "gqa": dict(desc="causal GQA bf16 B4 S4096 Hq32 Hkv8 D128", dtype="bf16", bound="mfma",
@@ -97,6 +98,143 @@ def make_gpu_case(name, dev, seed=0):
         v = normal((4, 4096, 8, 128), dtype=BF)
         return (lambda i: ops.gqa(q, k, v, causal=True)), [q, k, v]
     raise KeyError(name)
+
+
+# ----------------------------------------------------------------- NKIBench shapes
+# The reference's fp32 operator set at its own shapes, reported beside the graded
+# configurations.  Split GEMMs run three bf16 MFMA products per fp32 product
+# (hi*hi + hi*lo + lo*hi), so their roofline work is the MFMA flops issued; the
+# fp32-equivalent rate 2*M*N*K / t is reported as well.
+def _mm(m, k, n):
+    return 2 * m * k * n
+
+
+NKIBENCH = {
+    "silu": dict(desc="x[4096,7168]", dims=dict(M=4096, N=7168), bound="hbm", work=4096 * 7168 * 8),
+    "adamw": dict(desc="theta,g,m,v [10944,2048] -> new theta, step 1", dims=dict(M=10944, N=2048), bound="hbm",
+                  work=10944 * 2048 * 20),  # reads 4 arrays, writes 1
+    "rope_single_freq_apply": dict(desc="x[128,262144], cos/sin[64,262144]", dims=dict(D=128, S=262144),
+                                   bound="hbm",
+                                   work=3 * 128 * 262144 * 4),
+    "mamba": dict(desc="delta,u[256,7168] a[256,16] b,c[16,7168]", dims=dict(C=256, M=7168, S=16),
+                  bound="hbm",
+                  work=4 * (3 * 256 * 7168 + 256 * 16 + 2 * 16 * 7168),
+                  note="sequential over 7168 steps per (channel, state): latency-bound"),
+    "matmul": dict(desc="[4096,5120]@[5120,12288]", dims=dict(M=4096, K=5120, N=12288), bound="mfma", useful=_mm(4096, 5120, 12288),
+                   work=3 * _mm(4096, 5120, 12288)),
+    "transpose_matmul": dict(desc="[2048,4096]^T@[2048,10944]", dims=dict(M=4096, K=2048, N=10944),
+                             bound="mfma",
+                             useful=_mm(4096, 2048, 10944), work=3 * _mm(4096, 2048, 10944)),
+    "lora": dict(desc="x[4096,5120] w[5120,12288] a[5120,128] b[128,12288]",
+                 dims=dict(M=4096, K=5120, N=12288, R=128), bound="mfma",
+                 useful=_mm(4096, 5120, 12288) + _mm(4096, 5120, 128) + _mm(4096, 128, 12288),
+                 work=3 * (_mm(4096, 5120, 12288) + _mm(4096, 5120, 128) + _mm(4096, 128, 12288))),
+    "rmsnorm_matmul": dict(desc="x[4096,1024] w[1024,2048]", dims=dict(M=4096, K=1024, N=2048), bound="mfma",
+                           useful=_mm(4096, 1024, 2048), work=3 * _mm(4096, 1024, 2048)),
+    "add_rmsnorm_matmul": dict(desc="x,z[4096,1024] w[1024,2048], eps 1e-5", dims=dict(M=4096, K=1024, N=2048),
+                               eps=1e-5, bound="mfma",
+                               useful=_mm(4096, 1024, 2048), work=3 * _mm(4096, 1024, 2048)),
+    "matmul_add_rmsnorm": dict(desc="x[4096,2048] w[2048,2048] z[4096,2048], eps 1e-5",
+                               dims=dict(M=4096, K=2048, N=2048), eps=1e-5, bound="mfma",
+                               useful=_mm(4096, 2048, 2048), work=3 * _mm(4096, 2048, 2048)),
+    "swiglu": dict(desc="x[4096,1024] Wu,Wg[1024,3072] Wd[3072,1024]", dims=dict(M=4096, K=1024, N=3072),
+                   bound="mfma",
+                   useful=3 * _mm(4096, 1024, 3072), work=9 * _mm(4096, 1024, 3072)),
+    "bmm": dict(desc="[16,4096,64]@[16,64,4096]", dims=dict(B=16, M=4096, K=64, N=4096), bound="hbm",
+                work=4 * (2 * 16 * 4096 * 64 + 16 * 4096 * 4096)),
+    "bmm_softmax": dict(desc="softmax([16,4096,64]@[16,64,4096], -1)", dims=dict(B=16, M=4096, K=64, N=4096),
+                        bound="hbm",
+                        work=4 * (2 * 16 * 4096 * 64 + 16 * 4096 * 4096)),
+}
+
+
+def make_nki_case(name, dev, seed=0):
+    """NKIBench-shape fp32 inputs drawn on the GPU (N(0,1); mamba N(0,0.05);
+    AdamW v = |N(0,1)|).  Memory-bound ops rotate input sets larger than the
+    Infinity Cache in total."""
+    import torch
+    from kda import ops
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+
+    def draw(nsets=1, std=1.0):
+        shapes = _nki_shapes(name, NKIBENCH[name]["dims"])
+        return [[torch.randn(s, generator=g, device=dev) * std for s in shapes] for _ in range(nsets)]
+
+    if name == "silu":
+        sets = draw(3)
+        return (lambda i: ops.silu(*sets[i % 3])), sets
+    if name == "adamw":
+        sets = draw(2)
+        for st in sets:
+            st[3].abs_()
+        return (lambda i: ops.adamw(*sets[i % 2])), sets
+    if name == "rope_single_freq_apply":
+        sets = draw(2)
+        return (lambda i: ops.rope_single_freq_apply(*sets[i % 2])), sets
+    if name == "mamba":
+        sets = draw(2, std=0.05)
+        return (lambda i: ops.mamba(*sets[i % 2])), sets
+    (args,) = draw(1)
+    fn = getattr(ops, name)
+    if name in ("add_rmsnorm_matmul", "matmul_add_rmsnorm"):
+        x, w, z, gg = args
+        eps = NKIBENCH[name]["eps"]
+        return (lambda i: fn(x, w, eps, z, gg)), args
+    return (lambda i: fn(*args)), args
+
+
+def _nki_shapes(name, d):
+    if name == "silu":
+        return [(d["M"], d["N"])]
+    if name == "adamw":
+        return [(d["M"], d["N"])] * 4
+    if name == "rope_single_freq_apply":
+        return [(d["D"], d["S"]), (d["D"] // 2, d["S"]), (d["D"] // 2, d["S"])]
+    if name == "mamba":
+        C, M, S = d["C"], d["M"], d["S"]
+        return [(C, M), (C, M), (C, S), (S, M), (S, M)]
+    if name == "matmul":
+        return [(d["M"], d["K"]), (d["K"], d["N"])]
+    if name == "transpose_matmul":
+        return [(d["K"], d["M"]), (d["K"], d["N"])]
+    if name in ("bmm", "bmm_softmax"):
+        return [(d["B"], d["M"], d["K"]), (d["B"], d["K"], d["N"])]
+    if name == "lora":
+        return [(d["M"], d["K"]), (d["K"], d["N"]), (d["K"], d["R"]), (d["R"], d["N"])]
+    if name == "rmsnorm_matmul":
+        return [(d["M"], d["K"]), (d["K"], d["N"])]
+    if name in ("add_rmsnorm_matmul", "matmul_add_rmsnorm"):
+        M, K, N = d["M"], d["K"], d["N"]
+        gdim = K if name == "add_rmsnorm_matmul" else N
+        zshape = (M, K) if name == "add_rmsnorm_matmul" else (M, N)
+        return [(M, K), (K, N), zshape, (gdim,)]
+    if name == "swiglu":
+        M, K, N = d["M"], d["K"], d["N"]
+        return [(M, K), (K, N), (N, K), (K, N)]
+    raise KeyError(name)
+
+
+def nki_cpu_baseline(name, reps=3):
+    """The oracle (numpy) forward of an NKIBench op on this host; bmm_softmax and
+    bmm on 2 of the 16 batches, scaled x8.  Returns (ms, sample description)."""
+    import numpy as np
+    from oracle import inputs as oi
+    from oracle import ops as oo
+    dims = None
+    scale = 1
+    if name in ("bmm", "bmm_softmax"):
+        dims, scale = dict(B=2), 8
+    d = oi.draw(name, 0, dims=dims)
+    fn = getattr(oo, name)
+    fn(**d)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn(**d)
+        ts.append(time.perf_counter() - t0)
+    ms = sorted(ts)[len(ts) // 2] * 1e3 * scale
+    return ms, ("full shape" if scale == 1 else f"2 of 16 batches, scaled x{scale}")
 
 
 # ----------------------------------------------------------------- CPU baseline
@@ -157,6 +295,8 @@ def main():
     ap.add_argument("--iters", type=int, default=50, help="timed reps per op for the p50")
     ap.add_argument("--ops", default=",".join(CONFIGS), help="comma-separated subset")
     ap.add_argument("--no-cpu", action="store_true", help="skip the host numpy baseline")
+    ap.add_argument("--nki", default=",".join(NKIBENCH),
+                    help="comma-separated NKIBench-shape ops to report beside the configs ('' for none)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -214,6 +354,28 @@ def main():
             cpu[n] = dict(p50_ms=ms, sample=sample)
             log(f"[bench] cpu {n:15s} p50={ms:10.1f} ms  ({sample})")
 
+    nki = {}
+    for n in [x for x in args.nki.split(",") if x]:
+        cfg = NKIBENCH[n]
+        log(f"[bench] nkibench {n}")
+        fn, keep = make_nki_case(n, dev)
+        t = harness.time_op(fn, warmup=10, iters=max(20, args.iters // 2), device=dev)
+        rl = harness.roofline(cfg["work"], t.p50_ms * 1e-3, cfg["bound"])
+        row = dict(shape=cfg["desc"], p50_ms=round(t.p50_ms, 5), bound=cfg["bound"],
+                   achieved=round(rl["achieved"], 1), unit=rl["unit"], roofline_frac=round(rl["frac"], 4))
+        if "useful" in cfg:
+            row["fp32_tflops"] = round(cfg["useful"] / (t.p50_ms * 1e-3) / 1e12, 1)
+        if "note" in cfg:
+            row["note"] = cfg["note"]
+        del fn, keep
+        torch.cuda.empty_cache()
+        if not args.no_cpu:
+            ms, sample = nki_cpu_baseline(n)
+            row.update(cpu_p50_ms=round(ms, 2), cpu_sample=sample, speedup_vs_numpy=round(ms / t.p50_ms, 1))
+        log(f"[bench] nki {n:20s} p50={t.p50_ms * 1e3:9.1f} us  {rl['achieved']:8.1f} {rl['unit']}  "
+            f"frac={rl['frac']:.3f}  cpu={row.get('cpu_p50_ms')} ms")
+        nki[n] = row
+
     speedups = {n: cpu[n]["p50_ms"] / results[n]["p50_ms"] for n in names if n in cpu}
     geo = harness.geomean(list(speedups.values())) if speedups else None
     dominant = max(names, key=lambda n: results[n]["p50_ms"])
@@ -247,6 +409,9 @@ def main():
                         cpu_p50_ms=(round(cpu[n]["p50_ms"], 2) if n in cpu else None),
                         speedup_vs_numpy=(round(speedups[n], 1) if n in speedups else None))
                 for n in names},
+        "nkibench": nki or None,
+        "nkibench_geomean_speedup": (harness.geomean([r["speedup_vs_numpy"] for r in nki.values()])
+                                     if nki and not args.no_cpu else None),
     }
     print(json.dumps(line), flush=True)
     return 0
