@@ -38,6 +38,7 @@ constexpr int kWaves = kGroup * (kBM / kWaveRows);
 constexpr int kThreads = 64 * kWaves;
 constexpr int kKChunks = kBN * kD / 8 / kThreads;   // 16B K chunks staged per thread
 constexpr int kVUnits = (kBN / 2) * (kD / 8) / kThreads;  // (2 key x 8 d) V units per thread
+constexpr float kLazy = 8.0f;  // running-max slack (log2 units) before O and l are rescaled
 
 struct Args {
   const uint16_t* q;   // [B][S][Hq][D] (strides below, in elements)
@@ -192,47 +193,67 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
     }
 
     // ---- online softmax (rows: it*16 + l16; this lane's keys: 32c + 8g + 4hh + r)
+    // Scores stay unscaled; p = exp2(s*scale_log2 - m*scale_log2) is one FMA and
+    // one v_exp_f32.  The running max m is raised lazily: only when some row's
+    // tile max exceeds it by more than kLazy (in log2 units), so p <= 2^kLazy,
+    // which bf16 P and the fp32 row sums carry exactly as well; the final O / l
+    // cancels whichever m was used.  O and l are then rescaled for the whole wave
+    // (a wave-uniform branch), otherwise not at all.
     const int j_base = kt * kBN;
-    const bool diag = CAUSAL && (j_base + kBN - 1 > w0);
-    const bool tail = j_base + kBN > p.seq;
+    if ((CAUSAL && j_base + kBN - 1 > w0) || j_base + kBN > p.seq) {
+#pragma unroll
+      for (int it = 0; it < kIT; ++it) {
+        const int qrow = w0 + it * 16 + l16;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = j_base + 32 * (t >> 1) + 8 * g + 4 * (t & 1) + r;
+            if ((CAUSAL && key > qrow) || key >= p.seq) s[it][t][r] = -INFINITY;
+          }
+      }
+    }
+    float mx[kIT];
+    bool grow = false;
+#pragma unroll
+    for (int it = 0; it < kIT; ++it) {
+      float m = fmaxf(fmaxf(s[it][0][0], s[it][0][1]), fmaxf(s[it][0][2], s[it][0][3]));
+#pragma unroll
+      for (int t = 1; t < 4; ++t)
+        m = fmaxf(m, fmaxf(fmaxf(s[it][t][0], s[it][t][1]), fmaxf(s[it][t][2], s[it][t][3])));
+      m = fmaxf(m, __shfl_xor(m, 16));
+      m = fmaxf(m, __shfl_xor(m, 32));
+      mx[it] = m;
+      grow |= (m - m_run[it]) * p.scale_log2 > kLazy;
+    }
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+      for (int it = 0; it < kIT; ++it) {
+        const float m_new = fmaxf(m_run[it], mx[it]);
+        // rows with every key so far masked keep m = -inf: alpha = 0 then (O, l are 0)
+        const float alpha = (m_new == -INFINITY)
+                                ? 1.f
+                                : __builtin_amdgcn_exp2f((m_run[it] - m_new) * p.scale_log2);
+        m_run[it] = m_new;
+        l_run[it] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o_acc[it][dt] *= alpha;
+      }
+    }
     bf16x8 pf[kIT][2];   // [i-tile][32-key chunk]
 #pragma unroll
     for (int it = 0; it < kIT; ++it) {
-      const int qrow = w0 + it * 16 + l16;
-      float mx = -INFINITY;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float x = s[it][t][r] * p.scale_log2;
-          if (diag || tail) {
-            const int key = j_base + 32 * (t >> 1) + 8 * g + 4 * (t & 1) + r;
-            if ((CAUSAL && key > qrow) || key >= p.seq) x = -INFINITY;
-          }
-          s[it][t][r] = x;
-          mx = fmaxf(mx, x);
-        }
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run[it], mx);
-      // Rows with every key so far masked keep m = -inf; use 0 as the shift so
-      // exp2(-inf - 0) = 0 instead of NaN.
-      const float shift = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = exp2f(m_run[it] - shift);
-      m_run[it] = m_new;
+      const float shift = (m_run[it] == -INFINITY) ? 0.f : m_run[it] * p.scale_log2;
       float rs = 0.f;
       float pv[4][4];
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          pv[t][r] = exp2f(s[it][t][r] - shift);
+          pv[t][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[it][t][r], p.scale_log2, -shift));
           rs += pv[t][r];
         }
-      l_run[it] = l_run[it] * alpha + rs;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) o_acc[it][dt] *= alpha;
+      l_run[it] += rs;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         typedef float floatx2 __attribute__((ext_vector_type(2)));

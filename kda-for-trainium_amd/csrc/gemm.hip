@@ -47,6 +47,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "lds_dma.h"
 
 namespace kda {
 namespace gemm {
@@ -60,10 +61,8 @@ constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
 constexpr int kMaxSeg = 6;
 
-typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-#define KDA_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
 // 16 zero bytes: the DMA source for k-chunks past K (so they contribute 0).
 __device__ __align__(16) uint32_t g_zero_chunk[4] = {0u, 0u, 0u, 0u};
@@ -104,9 +103,6 @@ struct Params {
 // one chunk) at the LDS's 256 B/clk ds_read_b128 rate.
 template <int BK>
 __device__ __forceinline__ int kswz(int r) { return BK == 32 ? ((r >> 1) & 3) : (r & 7); }
-// Position of 32-byte segment s of k-row k in an MN-contiguous tile (measured
-// conflict-free for the ds_read_b64_tr_b16 fragment read).
-__device__ __forceinline__ int mswz(int k) { return (k & 3) | (((k >> 3) & 1) << 2); }
 
 // Maps the linear workgroup id to (tile_m, tile_n): XCD-contiguous, grouped by rows.
 __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
@@ -127,55 +123,6 @@ __device__ __forceinline__ float silu_f(float x) { return __fdividef(x, 1.0f + _
 
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2{lo, hi}), bf16x2));
-}
-
-// One 16-byte-per-lane DMA from global memory into LDS: lane i's 16 bytes at
-// `sbase + voff` land at LDS byte `lds + 16*i`.  The leading s_nop covers the
-// M0-write hazard.
-__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds) {
-  // the base is wave-uniform by construction; readfirstlane makes that visible
-  // (readfirstlane returns a signed int: widen through uint32_t, never sign-extend)
-  const uint64_t v = reinterpret_cast<uint64_t>(sbase);
-  const uint64_t u =
-      ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32)) << 32) |
-      (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff),
-               "s"(reinterpret_cast<const void*>(u)), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
-               : "memory");
-}
-// Same with a per-lane 64-bit address (used for the K tail, where lanes past K
-// read a zero chunk).
-__device__ __forceinline__ void dma16_ptr(const void* src, uint32_t lds) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)KDA_LDS_PTR(p);
-}
-
-// Reads the MFMA fragment (column `col0 + lane%16`, k = kbase + 8*(lane/16) .. +7)
-// of an MN-contiguous [BK][COLS] tile; col0 is a multiple of 16.
-template <int COLS>
-__device__ __forceinline__ bf16x8 read_mn_frag(const uint8_t* tile, int col0, int kbase, int lane) {
-  const int g = lane >> 4, jj = lane & 15;
-  const int s = col0 >> 4;
-  const int k0 = kbase + 8 * g + (jj >> 2);
-  const int k1 = k0 + 4;
-  const uint8_t* p0 = tile + k0 * (2 * COLS) + ((s ^ mswz(k0)) << 5) + 8 * (jj & 3);
-  const uint8_t* p1 = tile + k1 * (2 * COLS) + ((s ^ mswz(k1)) << 5) + 8 * (jj & 3);
-  const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) v4i16*)KDA_LDS_PTR(p0));
-  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) v4i16*)KDA_LDS_PTR(p1));
-  typedef short v8i16 __attribute__((ext_vector_type(8)));
-  const v8i16 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-  return __builtin_bit_cast(bf16x8, v);
 }
 
 // Reads the MFMA fragment (row `row`, k = kbase + 8*(lane/16) .. +7) of a
