@@ -7,23 +7,32 @@
 // Work decomposition: one workgroup = (batch b, kv head, block of 64 queries);
 // its 8 waves are the 4 query heads of that kv head (G == 4) x 2 halves of the
 // query block (32 rows each), so each K/V tile staged in LDS is read by the
-// whole query-head group.  32 rows per wave keep the O accumulators, scores and
-// Q fragments within the 256 VGPRs a wave has at 2 waves per SIMD.  Keys advance in tiles of
-// 64 through a double-buffered LDS ring with a register prefetch of the next
-// tile (one barrier per tile).  Causal blocks with the most key tiles are
-// scheduled first.
+// whole query-head group.  Causal blocks with the most key tiles are scheduled
+// first.
+//
+// Staging: K and V tiles of 64 keys go straight from global memory into LDS
+// (global_load_lds_dwordx4, no register staging), each through a 2-slot ring; the
+// LDS swizzle is applied on the global side by choosing which 16-byte chunk each
+// lane fetches.  K is stored [key][d] (16-byte chunk c of row r at c ^ kswz(r)); V
+// keeps its HBM orientation [key][d] (32-byte segment s of row r at s ^ mswz(r))
+// and its fragments are read transposed (ds_read_b64_tr_b16).
 //
 // Per wave (32 query rows x 64 keys per tile, head dim 128):
 //   S^T = K Q^T on v_mfma_f32_16x16x32_bf16 with K as the MFMA A operand: lane l
 //   then holds 4 keys of query row (l & 15) per 16x16 tile.  K rows are read in a
 //   permuted order so that, per 32-key chunk, each lane's 8 probabilities are 8
-//   consecutive keys -> they form the MFMA operand of O^T += V^T P^T directly
-//   (no LDS round trip for P).  V is transposed while being staged (LDS holds
-//   V^T, key-contiguous) so that one ds_read_b128 yields a V^T fragment.
-//   Online softmax in fp32 with exp2 (scale pre-multiplied by log2 e); the row
-//   max is reduced across the 4 lanes sharing a row, the row sum stays per-lane
-//   and is reduced once at the end.
+//   consecutive keys -> they form the B operand of O^T += V^T P^T directly
+//   (no LDS round trip for P).  A ninth O^T tile multiplies P by ones: it
+//   accumulates the row sums of the same bf16 probabilities on the MFMA.
+//   Online softmax in fp32: p = exp2(s*scale*log2e - m*scale*log2e) (one FMA and
+//   one v_exp_f32); the running max is raised lazily (only when a tile max exceeds
+//   it by more than 2^kLazy), so O is rescaled only then.  Masking is applied only
+//   on tiles that cross the causal diagonal or the sequence end.
+//   Software pipeline: iteration kt issues the MFMAs of O += V(kt-1) P(kt-1) and
+//   S(kt+1) = K(kt+1) Q^T in the same basic block as the softmax VALU work of
+//   S(kt), so a wave's MFMAs execute while it issues its VALU work.
 #include "common.h"
+#include "lds_dma.h"
 
 namespace kda {
 namespace attn {
@@ -36,9 +45,10 @@ constexpr int kBN = 64;       // keys per tile
 constexpr int kGroup = 4;     // query heads per kv head
 constexpr int kWaves = kGroup * (kBM / kWaveRows);
 constexpr int kThreads = 64 * kWaves;
-constexpr int kKChunks = kBN * kD / 8 / kThreads;   // 16B K chunks staged per thread
-constexpr int kVUnits = (kBN / 2) * (kD / 8) / kThreads;  // (2 key x 8 d) V units per thread
-constexpr float kLazy = 8.0f;  // running-max slack (log2 units) before O and l are rescaled
+constexpr int kTileBytes = kBN * kD * 2;                    // one K or V tile: 16 KiB
+constexpr int kDmaPerWave = kTileBytes / (kWaves * 1024);   // DMA instructions per wave per tile
+constexpr int kDT = kD / 16 + 1;                            // O^T tiles: 8 of d + the row sums
+constexpr float kLazy = 8.0f;  // running-max slack (log2 units) before O is rescaled
 
 struct Args {
   const uint16_t* q;   // [B][S][Hq][D] (strides below, in elements)
@@ -52,18 +62,185 @@ struct Args {
   float scale_log2;    // softmax scale * log2(e)
 };
 
-// Swizzled 16-byte chunk within a K row (16 chunks of 8 d): conflict-free for the
-// permuted 16-row fragment reads below (rows 32c + 8a + r, a, r in 0..3).
-__device__ __forceinline__ int k_swz(int row, int chunk) {
-  return chunk ^ ((row & 3) | (((row >> 3) & 3) << 2));
+// Swizzle of the 16 16-byte chunks of a K row: conflict-free for the permuted
+// 16-row fragment read (rows 32c + 8a + 4hh + r, a, r in 0..3, one chunk).
+__device__ __forceinline__ int kswz(int row) { return (row & 3) | (((row >> 3) & 3) << 2); }
+
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2{lo, hi}), bf16x2));
 }
-// Swizzled 16-byte chunk within a V^T row (8 chunks of 8 keys).
-__device__ __forceinline__ int v_swz(int row, int chunk) { return chunk ^ (row & 7); }
+
+// max over the four lanes that share a query row (lanes l, l^16, l^32, l^48)
+__device__ __forceinline__ float row_max4(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  x = fmaxf(__builtin_bit_cast(float, a[0]), __builtin_bit_cast(float, a[1]));
+  const uint32_t w = __builtin_bit_cast(uint32_t, x);
+  const auto c = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+  return fmaxf(__builtin_bit_cast(float, c[0]), __builtin_bit_cast(float, c[1]));
+}
+
+// Per-wave state carried across key tiles.
+struct State {
+  bf16x8 qf[kIT][4];      // Q fragments (MFMA B operand): row it*16 + l16, d = dc*32 + 8g .. +8
+  floatx4 o[kIT][kDT];    // O^T: lane holds row l16, d = dt*16 + 4g + r; tile 8 = row sums
+  float m[kIT];           // running max (raw score units)
+};
+
+__device__ __forceinline__ bf16x8 k_frag(const uint8_t* kt_lds, int t, int dc, int lane) {
+  const int l16 = lane & 15, g = lane >> 4;
+  const int krow = 32 * (t >> 1) + 8 * (l16 >> 2) + 4 * (t & 1) + (l16 & 3);
+  return *reinterpret_cast<const bf16x8*>(kt_lds + krow * (2 * kD) +
+                                          (((dc * 4 + g) ^ kswz(krow)) << 4));
+}
+
+// S^T = K Q^T: s[it][t], t = 2c + hh covers keys 32c + 8a + 4hh + r for A-row 4a + r.
+// d-chunk outer: the 8 accumulators rotate, consecutive MFMAs are independent.
+__device__ __forceinline__ void scores(const State& st, const uint8_t* k_lds, int lane,
+                                       floatx4 (&s)[kIT][4]) {
+#pragma unroll
+  for (int it = 0; it < kIT; ++it)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) s[it][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int dc = 0; dc < 4; ++dc)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const bf16x8 kf = k_frag(k_lds, t, dc, lane);
+#pragma unroll
+      for (int it = 0; it < kIT; ++it)
+        s[it][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, st.qf[it][dc], s[it][t], 0, 0, 0);
+    }
+}
+
+// O^T += V^T P^T (V^T fragment: row d = dt*16 + l16, keys 32c + 8g .. +8), plus the
+// row sums ones^T P^T.
+__device__ __forceinline__ void accumulate_pv(State& st, const uint8_t* v_lds,
+                                              const bf16x8 (&pf)[kIT][2], int lane) {
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const bf16x8 vf = read_mn_frag<kD>(v_lds, dt * 16, 32 * c, lane);
+#pragma unroll
+      for (int it = 0; it < kIT; ++it)
+        st.o[it][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[it][c], st.o[it][dt], 0, 0, 0);
+    }
+  bf16x8 ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = (__bf16)1.0f;
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int it = 0; it < kIT; ++it)
+      st.o[it][kDT - 1] =
+          __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[it][c], st.o[it][kDT - 1], 0, 0, 0);
+}
+
+// Online softmax of S(kt), first half: masking, row maxima and the running-max
+// update.  Returns whether the running max of some row was raised (then alpha
+// holds the factor O must be multiplied by) and leaves shift = m * scale_log2.
+template <bool CAUSAL, bool MASK>
+__device__ __forceinline__ bool softmax_stats(State& st, const Args& p, int kt, int w0, int lane,
+                                              floatx4 (&s)[kIT][4], float (&alpha)[kIT],
+                                              float (&shift)[kIT]) {
+  const int l16 = lane & 15, g = lane >> 4;
+  if constexpr (MASK) {
+    const int j_base = kt * kBN;
+#pragma unroll
+    for (int it = 0; it < kIT; ++it) {
+      const int qrow = w0 + it * 16 + l16;
+      // keys of this lane: j_base + 32(t>>1) + 8g + 4(t&1) + r; masked if > lim
+      const int lim = (CAUSAL ? min(qrow, p.seq - 1) : p.seq - 1) - j_base - 8 * g;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (32 * (t >> 1) + 4 * (t & 1) + r > lim) s[it][t][r] = -INFINITY;
+    }
+  }
+  bool grow_any = false;
+#pragma unroll
+  for (int it = 0; it < kIT; ++it) {
+    float m = __builtin_fmaxf(__builtin_fmaxf(s[it][0][0], s[it][0][1]), s[it][0][2]);
+    m = __builtin_fmaxf(__builtin_fmaxf(m, s[it][0][3]), s[it][1][0]);
+#pragma unroll
+    for (int t = 1; t < 4; ++t)
+#pragma unroll
+      for (int r = (t == 1 ? 1 : 0); r < 4; r += 2) {
+        if (r + 1 < 4)
+          m = __builtin_fmaxf(__builtin_fmaxf(m, s[it][t][r]), s[it][t][r + 1]);
+        else
+          m = __builtin_fmaxf(m, s[it][t][r]);
+      }
+    m = row_max4(m);
+    // per-row decision (the four lanes of a row agree): a lane-divergent select,
+    // so nothing here becomes a branch and the block stays whole for scheduling
+    const bool grow = (m - st.m[it]) * p.scale_log2 > kLazy;
+    grow_any |= grow;
+    const float m_new = grow ? __builtin_fmaxf(st.m[it], m) : st.m[it];
+    // a row whose keys so far are all masked keeps m = -inf (its O is 0)
+    const float e = __builtin_amdgcn_exp2f((st.m[it] - m_new) * p.scale_log2);
+    alpha[it] = (m_new == -INFINITY) ? 1.f : e;
+    st.m[it] = m_new;
+    shift[it] = (m_new == -INFINITY) ? 0.f : m_new * p.scale_log2;
+  }
+  const bool any = __builtin_amdgcn_ballot_w64(grow_any) != 0;
+  (void)g;
+  return any;
+}
+
+// Second half: probabilities p = exp2(s*scale_log2 - shift), packed to bf16 as the
+// B operand of O^T += V^T P^T.
+__device__ __forceinline__ void softmax_probs(const Args& p, const floatx4 (&s)[kIT][4],
+                                              const float (&shift)[kIT], bf16x8 (&pf)[kIT][2]) {
+#pragma unroll
+  for (int it = 0; it < kIT; ++it) {
+    float pv[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        pv[t][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[it][t][r], p.scale_log2, -shift[it]));
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      u32x4 w;
+      w[0] = pack2(pv[2 * c][0], pv[2 * c][1]);
+      w[1] = pack2(pv[2 * c][2], pv[2 * c][3]);
+      w[2] = pack2(pv[2 * c + 1][0], pv[2 * c + 1][1]);
+      w[3] = pack2(pv[2 * c + 1][2], pv[2 * c + 1][3]);
+      pf[it][c] = __builtin_bit_cast(bf16x8, w);
+    }
+  }
+}
+
+template <bool CAUSAL, bool MASK>
+__device__ __forceinline__ bool softmax(State& st, const Args& p, int kt, int w0, int lane,
+                                        floatx4 (&s)[kIT][4], bf16x8 (&pf)[kIT][2],
+                                        float (&alpha)[kIT]) {
+  float shift[kIT];
+  const bool any = softmax_stats<CAUSAL, MASK>(st, p, kt, w0, lane, s, alpha, shift);
+  softmax_probs(p, s, shift, pf);
+  return any;
+}
+
+// Scheduling hint for one steady-state iteration (68 MFMAs next to ~100 VALU and
+// transcendental instructions of the softmax): alternate one MFMA with a few
+// VALU/TRANS instructions, so the softmax issues while the MFMA pipe is busy.
+__device__ __forceinline__ void interleave_hint() {
+#pragma unroll
+  for (int i = 0; i < 68; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x402, 2, 0);   // VALU | TRANS
+  }
+}
 
 template <bool CAUSAL>
 __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
-  __shared__ __align__(16) uint16_t Ks[2][kBN * kD];   // [key][d]    (swizzled chunks)
-  __shared__ __align__(16) uint16_t Vt[2][kD * kBN];   // [d][key]    (swizzled chunks)
+  __shared__ __align__(1024) uint8_t smem[4 * kTileBytes];   // K slots 0,1; V slots 2,3
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -81,227 +258,165 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   const int q0 = qb * kBM;
   const int w0 = q0 + (wave / kGroup) * kWaveRows;   // this wave's first query row
 
-  const uint16_t* qp = p.q + b * p.q_sb + (int64_t)h * kD;
-  const uint16_t* kp = p.k + b * p.k_sb + (int64_t)kvh * kD;
-  const uint16_t* vp = p.v + b * p.k_sb + (int64_t)kvh * kD;
-
-  // ---- Q fragments (MFMA B operand): row q0 + it*16 + l16, d = dc*32 + 8g .. +8
-  bf16x8 qf[kIT][4];
+  State st;
+  {
+    const uint16_t* qp = p.q + b * p.q_sb + (int64_t)h * kD;
 #pragma unroll
-  for (int it = 0; it < kIT; ++it) {
-    const int row = w0 + it * 16 + l16;
+    for (int it = 0; it < kIT; ++it) {
+      const int row = w0 + it * 16 + l16;
 #pragma unroll
-    for (int dc = 0; dc < 4; ++dc) {
-      if (row < p.seq)
-        qf[it][dc] = *reinterpret_cast<const bf16x8*>(qp + row * p.q_ss + dc * 32 + g * 8);
-      else
-        qf[it][dc] = bf16x8{};
+      for (int dc = 0; dc < 4; ++dc)
+        st.qf[it][dc] = (row < p.seq)
+                            ? *reinterpret_cast<const bf16x8*>(qp + row * p.q_ss + dc * 32 + g * 8)
+                            : bf16x8{};
+    }
+#pragma unroll
+    for (int it = 0; it < kIT; ++it) {
+#pragma unroll
+      for (int dt = 0; dt < kDT; ++dt) st.o[it][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      st.m[it] = -INFINITY;
     }
   }
 
-  // ---- K/V staging: kKChunks x 16B of K and kVUnits x (2 keys x 8 d) of V per thread
-  static_assert(kKChunks >= 1 && kVUnits >= 1, "staging split");
-  static_assert(kKChunks * kThreads * 8 == kBN * kD && kVUnits * kThreads * 16 == kBN * kD, "exact split");
-  u32x4 kreg[kKChunks], vreg[kVUnits][2];
-  auto load_kv = [&](int kt) {
+  // ---- DMA geometry: instruction j of this wave fills LDS bytes
+  // [(j*kWaves + wave)*1024, +1024) of a tile = rows 4q .. 4q+3, lane -> (row, chunk)
+  const int64_t row_bytes = p.k_ss * 2;
+  const char* kbase = reinterpret_cast<const char*>(p.k + b * p.k_sb + (int64_t)kvh * kD);
+  const char* vbase = reinterpret_cast<const char*>(p.v + b * p.k_sb + (int64_t)kvh * kD);
+  int drow[kDmaPerWave];
+  uint32_t kcol[kDmaPerWave], vcol[kDmaPerWave];
+#pragma unroll
+  for (int j = 0; j < kDmaPerWave; ++j) {
+    const int r = (j * kWaves + wave) * 4 + (lane >> 4);
+    const int t = lane & 15;
+    drow[j] = r;
+    kcol[j] = (uint32_t)((t ^ kswz(r)) << 4);
+    vcol[j] = (uint32_t)(((((t >> 1) ^ mswz(r)) << 5)) + ((t & 1) << 4));
+  }
+  // Rows past the sequence are clamped to the last key: their scores are
+  // masked and their V rows meet p = 0.
+  auto issue = [&](const char* base, const uint32_t (&col)[kDmaPerWave], int kt, uint32_t lds) {
     const int j0 = kt * kBN;
+    const char* tb = base + (int64_t)j0 * row_bytes;
+    const int last = p.seq - 1 - j0;
 #pragma unroll
-    for (int i = 0; i < kKChunks; ++i) {
-      const int c = tid + kThreads * i;
-      const int row = c >> 4, ch = c & 15;
-      const int j = j0 + row;
-      kreg[i] = (j < p.seq) ? *reinterpret_cast<const u32x4*>(kp + j * p.k_ss + ch * 8)
-                            : u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int u = 0; u < kVUnits; ++u) {
-      const int unit = tid + kThreads * u;
-      const int jp = unit & 31, dc = unit >> 5;   // keys jp*2..+2, d = dc*8..+8
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int j = j0 + jp * 2 + r;
-        vreg[u][r] = (j < p.seq) ? *reinterpret_cast<const u32x4*>(vp + j * p.k_ss + dc * 8)
-                                 : u32x4{0u, 0u, 0u, 0u};
-      }
-    }
+    for (int j = 0; j < kDmaPerWave; ++j)
+      dma16(tb, (uint32_t)(min(drow[j], last) * row_bytes) + col[j],
+            lds + (uint32_t)((j * kWaves + wave) * 1024));
   };
-  auto store_kv = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < kKChunks; ++i) {
-      const int c = tid + kThreads * i;
-      const int row = c >> 4, ch = c & 15;
-      *reinterpret_cast<u32x4*>(&Ks[buf][row * kD + k_swz(row, ch) * 8]) = kreg[i];
-    }
-#pragma unroll
-    for (int u = 0; u < kVUnits; ++u) {
-      const int unit = tid + kThreads * u;
-      const int jp = unit & 31, dc = unit >> 5;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = dc * 8 + e;
-        const int w = e >> 1;
-        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-        const uint32_t o = __builtin_amdgcn_perm(vreg[u][1][w], vreg[u][0][w], sel);
-        // keys jp*2..+2 -> 16B chunk jp/4, dword jp&3 within it
-        *reinterpret_cast<uint32_t*>(&Vt[buf][d * kBN + v_swz(d, jp >> 2) * 8 + (jp & 3) * 2]) = o;
-      }
-    }
-  };
-
-  floatx4 o_acc[kIT][8];   // [i-tile][d-tile]: O^T, lane holds row l16, d = dt*16 + 4g + r
-#pragma unroll
-  for (int it = 0; it < kIT; ++it)
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o_acc[it][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m_run[kIT], l_run[kIT];
-#pragma unroll
-  for (int it = 0; it < kIT; ++it) {
-    m_run[it] = -INFINITY;
-    l_run[it] = 0.f;
-  }
+  auto k_tile = [&](int kt) { return smem + (kt & 1) * kTileBytes; };
+  auto v_tile = [&](int kt) { return smem + (2 + (kt & 1)) * kTileBytes; };
 
   const int nkt_all = (p.seq + kBN - 1) / kBN;
   const int nkt = CAUSAL ? min(nkt_all, (q0 + kBM - 1) / kBN + 1) : nkt_all;
+  // tiles [0, nfree) need no mask for any row of this workgroup
+  int nfree = p.seq / kBN;                         // full tiles
+  if (CAUSAL) nfree = min(nfree, (q0 + 1) / kBN);  // keys j0+63 <= q0 for every row
+  nfree = min(nfree, nkt);
 
-  load_kv(0);
-  store_kv(0);
+  // Iteration kt (after the barrier that ends iteration kt-1) fetches K(kt+2) into
+  // the slot of K(kt) and V(kt) into the slot of V(kt-2) (both last read in
+  // iteration kt-1), then computes O += V(kt-1) P(kt-1), S(kt+1) and the softmax of
+  // S(kt); its DMAs complete before the barrier that ends it.
+  issue(kbase, kcol, 0, lds_addr(k_tile(0)));
+  if (nkt > 1) issue(kbase, kcol, 1, lds_addr(k_tile(1)));
+  wait_vmcnt<0>();
+  __syncthreads();
+  floatx4 s[kIT][4], s_next[kIT][4];
+  bf16x8 pf[kIT][2], pf_next[kIT][2];
+  float alpha[kIT];
+  scores(st, k_tile(0), lane, s);
   __syncthreads();
 
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int buf = kt & 1;
-    const bool more = kt + 1 < nkt;
-    if (more) load_kv(kt + 1);
-
-    // ---- S^T = K Q^T : tiles t = 2c + hh, keys 32c + 8a + 4hh + r for A-row 4a + r
-    floatx4 s[kIT][4];   // [i-tile][t]
+  auto fetch = [&](int kt) {
+    if (kt + 2 < nkt) issue(kbase, kcol, kt + 2, lds_addr(k_tile(kt + 2)));
+    issue(vbase, vcol, kt, lds_addr(v_tile(kt)));
+  };
+  // O moves to the running max set by the previous tile's statistics; done
+  // before the next O += V P (and at the top of an iteration, so the branch does
+  // not split the iteration's MFMA/softmax block).
+  auto rescale = [&](bool any) {
+    if (any) {
 #pragma unroll
-    for (int it = 0; it < kIT; ++it)
+      for (int it = 0; it < kIT; ++it)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) s[it][t] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int c = t >> 1, hh = t & 1;
-      const int krow = 32 * c + 8 * (l16 >> 2) + 4 * hh + (l16 & 3);
-#pragma unroll
-      for (int dc = 0; dc < 4; ++dc) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(
-            &Ks[buf][krow * kD + k_swz(krow, dc * 4 + g) * 8]);
-#pragma unroll
-        for (int it = 0; it < kIT; ++it)
-          s[it][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[it][dc], s[it][t], 0, 0, 0);
-      }
+        for (int dt = 0; dt < kDT; ++dt) st.o[it][dt] *= alpha[it];
     }
-
-    // ---- online softmax (rows: it*16 + l16; this lane's keys: 32c + 8g + 4hh + r)
-    // Scores stay unscaled; p = exp2(s*scale_log2 - m*scale_log2) is one FMA and
-    // one v_exp_f32.  The running max m is raised lazily: only when some row's
-    // tile max exceeds it by more than kLazy (in log2 units), so p <= 2^kLazy,
-    // which bf16 P and the fp32 row sums carry exactly as well; the final O / l
-    // cancels whichever m was used.  O and l are then rescaled for the whole wave
-    // (a wave-uniform branch), otherwise not at all.
-    const int j_base = kt * kBN;
-    if ((CAUSAL && j_base + kBN - 1 > w0) || j_base + kBN > p.seq) {
-#pragma unroll
-      for (int it = 0; it < kIT; ++it) {
-        const int qrow = w0 + it * 16 + l16;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int key = j_base + 32 * (t >> 1) + 8 * g + 4 * (t & 1) + r;
-            if ((CAUSAL && key > qrow) || key >= p.seq) s[it][t][r] = -INFINITY;
-          }
-      }
-    }
-    float mx[kIT];
-    bool grow = false;
+  };
+  auto finish = [&]() {
 #pragma unroll
     for (int it = 0; it < kIT; ++it) {
-      float m = fmaxf(fmaxf(s[it][0][0], s[it][0][1]), fmaxf(s[it][0][2], s[it][0][3]));
 #pragma unroll
-      for (int t = 1; t < 4; ++t)
-        m = fmaxf(m, fmaxf(fmaxf(s[it][t][0], s[it][t][1]), fmaxf(s[it][t][2], s[it][t][3])));
-      m = fmaxf(m, __shfl_xor(m, 16));
-      m = fmaxf(m, __shfl_xor(m, 32));
-      mx[it] = m;
-      grow |= (m - m_run[it]) * p.scale_log2 > kLazy;
+      for (int t = 0; t < 4; ++t) s[it][t] = s_next[it][t];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) pf[it][c] = pf_next[it][c];
     }
-    if (__builtin_amdgcn_ballot_w64(grow)) {
-#pragma unroll
-      for (int it = 0; it < kIT; ++it) {
-        const float m_new = fmaxf(m_run[it], mx[it]);
-        // rows with every key so far masked keep m = -inf: alpha = 0 then (O, l are 0)
-        const float alpha = (m_new == -INFINITY)
-                                ? 1.f
-                                : __builtin_amdgcn_exp2f((m_run[it] - m_new) * p.scale_log2);
-        m_run[it] = m_new;
-        l_run[it] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o_acc[it][dt] *= alpha;
-      }
-    }
-    bf16x8 pf[kIT][2];   // [i-tile][32-key chunk]
-#pragma unroll
-    for (int it = 0; it < kIT; ++it) {
-      const float shift = (m_run[it] == -INFINITY) ? 0.f : m_run[it] * p.scale_log2;
-      float rs = 0.f;
-      float pv[4][4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          pv[t][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[it][t][r], p.scale_log2, -shift));
-          rs += pv[t][r];
-        }
-      l_run[it] += rs;
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        typedef float floatx2 __attribute__((ext_vector_type(2)));
-        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-        u32x4 w;
-        w[0] = __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2{pv[2 * c][0], pv[2 * c][1]}), bf16x2));
-        w[1] = __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2{pv[2 * c][2], pv[2 * c][3]}), bf16x2));
-        w[2] = __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2{pv[2 * c + 1][0], pv[2 * c + 1][1]}), bf16x2));
-        w[3] = __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2{pv[2 * c + 1][2], pv[2 * c + 1][3]}), bf16x2));
-        pf[it][c] = __builtin_bit_cast(bf16x8, w);
-      }
-    }
-
-    // ---- O^T += V^T P^T
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const int d = dt * 16 + l16;
-        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&Vt[buf][d * kBN + v_swz(d, c * 4 + g) * 8]);
-#pragma unroll
-        for (int it = 0; it < kIT; ++it)
-          o_acc[it][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[it][c], o_acc[it][dt], 0, 0, 0);
-      }
-    }
-
-    if (more) store_kv(buf ^ 1);
+    wait_vmcnt<0>();
     __syncthreads();
-  }
+  };
 
-  // ---- normalise and store: lane holds out[row][d = dt*16 + 4g .. +4]
+  // kt = 0: no O update yet (O is 0; its first rescale multiplies zeros)
+  bool any;
+  {
+    fetch(0);
+    if (nkt > 1) scores(st, k_tile(1), lane, s_next);
+    float shift[kIT];
+    any = (nfree > 0) ? softmax_stats<CAUSAL, false>(st, p, 0, w0, lane, s, alpha, shift)
+                      : softmax_stats<CAUSAL, true>(st, p, 0, w0, lane, s, alpha, shift);
+    softmax_probs(p, s, shift, pf_next);
+    finish();
+  }
+  int kt = 1;
+  const int n_mid_free = min(nfree, nkt - 1);
+  for (; kt < n_mid_free; ++kt) {
+    fetch(kt);
+    rescale(any);
+    float shift[kIT];
+    any = softmax_stats<CAUSAL, false>(st, p, kt, w0, lane, s, alpha, shift);
+    accumulate_pv(st, v_tile(kt - 1), pf, lane);
+    scores(st, k_tile(kt + 1), lane, s_next);
+    softmax_probs(p, s, shift, pf_next);
+    interleave_hint();
+    finish();
+  }
+  for (; kt < nkt - 1; ++kt) {
+    fetch(kt);
+    rescale(any);
+    float shift[kIT];
+    any = softmax_stats<CAUSAL, true>(st, p, kt, w0, lane, s, alpha, shift);
+    accumulate_pv(st, v_tile(kt - 1), pf, lane);
+    scores(st, k_tile(kt + 1), lane, s_next);
+    softmax_probs(p, s, shift, pf_next);
+    interleave_hint();
+    finish();
+  }
+  if (kt == nkt - 1 && kt >= 1) {   // last tile: no S(kt+1)
+    fetch(kt);
+    rescale(any);
+    float shift[kIT];
+    any = (kt < nfree) ? softmax_stats<CAUSAL, false>(st, p, kt, w0, lane, s, alpha, shift)
+                       : softmax_stats<CAUSAL, true>(st, p, kt, w0, lane, s, alpha, shift);
+    accumulate_pv(st, v_tile(kt - 1), pf, lane);
+    softmax_probs(p, s, shift, pf_next);
+    finish();
+  }
+  rescale(any);
+  accumulate_pv(st, v_tile(nkt - 1), pf, lane);
+
+  // ---- normalise and store: lane holds out[row][d = dt*16 + 4g .. +4]; the row
+  // sum of its query row is in every element of the ninth O^T tile
   uint16_t* op = p.out + b * p.o_sb + (int64_t)h * p.o_sh;
 #pragma unroll
   for (int it = 0; it < kIT; ++it) {
-    float l = l_run[it];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    const float inv = 1.0f / l;
+    const float inv = 1.0f / st.o[it][kDT - 1][0];
     const int row = w0 + it * 16 + l16;
     if (row >= p.seq) continue;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      typedef float floatx2 __attribute__((ext_vector_type(2)));
-      typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-      const floatx4 o = o_acc[it][dt] * inv;
+    for (int dt = 0; dt < kDT - 1; ++dt) {
+      const floatx4 o = st.o[it][dt] * inv;
       u32x2 w;
-      w[0] = __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2{o[0], o[1]}), bf16x2));
-      w[1] = __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2{o[2], o[3]}), bf16x2));
+      w[0] = pack2(o[0], o[1]);
+      w[1] = pack2(o[2], o[3]);
       *reinterpret_cast<u32x2*>(op + row * p.o_ss + dt * 16 + 4 * g) = w;
     }
   }
