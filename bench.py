@@ -276,6 +276,18 @@ def cpu_baseline(name, reps=3):
     raise KeyError(name)
 
 
+def measured_traffic():
+    """HBM bytes per launch per configuration, from the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary committed under profiles/ (None when absent)."""
+    path = ROOT / "profiles" / "hbm_traffic_graded_configs.md"
+    try:
+        text = path.read_text()
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        return json.loads(block)
+    except (OSError, IndexError, ValueError):
+        return None
+
+
 def blas_threads():
     try:
         from threadpoolctl import threadpool_info
@@ -283,6 +295,30 @@ def blas_threads():
                    default=None)
     except Exception:
         return None
+
+
+# ----------------------------------------------------------------- profiling mode
+
+def run_cases(cases, reps, dev):
+    """Runs each case `reps` times (for rocprofv3 runs); prints one line per case."""
+    import torch
+    for name in cases:
+        if name.startswith("copy:"):
+            src = torch.randn((int(name[5:]) << 20) // 4, device=dev)
+            dst = torch.empty_like(src)
+            fn, keep = (lambda i: dst.copy_(src)), [src, dst]
+        elif name.startswith("nki:"):
+            fn, keep = make_nki_case(name[4:], dev)
+        else:
+            fn, keep = make_gpu_case(name, dev)
+        torch.cuda.synchronize()
+        for i in range(reps):
+            fn(i)
+        torch.cuda.synchronize()
+        log(f"[bench] ran {name} x{reps}")
+        del fn, keep
+        torch.cuda.empty_cache()
+    return 0
 
 
 # ----------------------------------------------------------------- main
@@ -297,6 +333,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the host numpy baseline")
     ap.add_argument("--nki", default=",".join(NKIBENCH),
                     help="comma-separated NKIBench-shape ops to report beside the configs ('' for none)")
+    ap.add_argument("--run", default=None,
+                    help="profiling mode: run the comma-separated cases --reps times each and exit "
+                         "(config names, nki:<op>, or copy:<MiB> for a device-to-device copy of "
+                         "known size, the reference for counter scaling)")
+    ap.add_argument("--reps", type=int, default=3)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -311,6 +352,8 @@ def main():
         log("bench.py: no GPU visible")
         return 1
     dev = torch.device("cuda", 0)
+    if args.run:
+        return run_cases(args.run.split(","), args.reps, dev)
     names = [n for n in args.ops.split(",") if n]
 
     cases = {}
@@ -380,7 +423,10 @@ def main():
     geo = harness.geomean(list(speedups.values())) if speedups else None
     dominant = max(names, key=lambda n: results[n]["p50_ms"])
     rl = dict(results[dominant]["roofline"])
-    rl.update(kernel=dominant, kernels=CONFIGS[dominant]["kernels"], traffic=None)
+    traffic = measured_traffic()
+    rl.update(kernel=dominant, kernels=CONFIGS[dominant]["kernels"],
+              traffic=(traffic or {}).get(dominant),
+              traffic_source="profiles/hbm_traffic_graded_configs.md (rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     cores = len(os.sched_getaffinity(0))
     line = {
         "metric": METRIC,
