@@ -183,10 +183,11 @@ int kda_swiglu_f32(const float* x, const float* w_up, const float* w_down, const
 
 /* out[b, m, :] = softmax_n(lhs[b, m, :] @ rhs[b, :, :]) (max-shifted), fp32; lhs
  * [B,M,K], rhs [B,K,N], out [B,M,N]; K <= 64, N a multiple of 64.  Scores on
- * bf16 MFMA from a three-limb split of both operands (six products, residual
- * ~2^-24: the softmax turns score errors into relative output errors); one
- * fused kernel computes online row statistics, then recomputes the scores and
- * writes the probabilities once.  Workspace: KDA_OP_BMM_SOFTMAX_F32.
+ * fp16 MFMA from a two-limb split of both operands after power-of-two scaling
+ * per lhs row and per 64-column rhs tile (three products, ~22 significant bits:
+ * the softmax turns score errors into relative output errors); one fused
+ * kernel computes online row statistics, then recomputes the scores and writes
+ * the probabilities once.  Workspace: KDA_OP_BMM_SOFTMAX_F32.
  * Replaces kernel(lhs, rhs) of workspaces/bmm_softmax/runs/bmm_softmax_v4.py:10-181
  * (forward workspaces/bmm_softmax/docs/draft-phase1.md:14-23). */
 int kda_bmm_softmax_f32(const float* lhs, const float* rhs, float* out, int64_t batch, int64_t m,

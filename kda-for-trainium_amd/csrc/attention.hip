@@ -32,6 +32,7 @@
 //   S(kt+1) = K(kt+1) Q^T in the same basic block as the softmax VALU work of
 //   S(kt), so a wave's MFMAs execute while it issues its VALU work.
 #include "common.h"
+#include "lanes.h"
 #include "lds_dma.h"
 
 namespace kda {
@@ -71,16 +72,6 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2{lo, hi}), bf16x2));
-}
-
-// max over the four lanes that share a query row (lanes l, l^16, l^32, l^48)
-__device__ __forceinline__ float row_max4(float x) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, x);
-  const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  x = fmaxf(__builtin_bit_cast(float, a[0]), __builtin_bit_cast(float, a[1]));
-  const uint32_t w = __builtin_bit_cast(uint32_t, x);
-  const auto c = __builtin_amdgcn_permlane16_swap(w, w, false, false);
-  return fmaxf(__builtin_bit_cast(float, c[0]), __builtin_bit_cast(float, c[1]));
 }
 
 // Per-wave state carried across key tiles.

@@ -5,22 +5,30 @@
 // lhs [B, M, K], rhs [B, K, N], out [B, M, N] fp32, K <= 64, N % 64 == 0.
 //
 // Precision.  The softmax turns absolute errors of the scores into relative
-// errors of the output, and the scores are O(sqrt(K)) large, so the two-limb
-// bf16 split used by the fp32 GEMMs (~1e-5 per product) is not enough.  Both
-// operands are split into three bf16 limbs (x = x0 + x1 + x2, residual ~2^-24)
-// and each score takes the six products x_i * y_j with i + j <= 2 on bf16 MFMA,
-// accumulated in fp32.
+// errors of the output, and the scores are O(sqrt(K)) large, so the scores need
+// close to fp32 accuracy.  Both operands are scaled by powers of two (each lhs
+// row, each 64-column tile of rhs, so that the largest |value| lies in
+// [2^13, 2^14)) and split into two fp16 limbs, x = x0 + x1 (22 significant
+// bits; fp16 keeps 11 bits per limb against bf16's 8).  A score takes the three
+// products x0*y0 + x0*y1 + x1*y0 on fp16 MFMA with fp32 accumulation; the
+// dropped x1*y1 and the residual below x1 are ~2^-22 of each product, and the
+// scaling is undone exactly by the power-of-two factor of (row, tile).  On the
+// NKIBench inputs this matches fp64 scores to within 2% of the error of the
+// fp32 reference itself.
 //
-// Work decomposition.  One workgroup = 128 rows of one batch (8 waves x 16 rows);
-// it streams the N axis in 64-column tiles of rhs^T (three bf16 limb planes,
-// [N][K] after the pre-pass split_transpose_kernel), DMA'd global->LDS into a
-// ring of three buffers and shared by the 8 waves.  Two passes over N:
-//   pass 0: online row max and sum of exp (flash-softmax statistics);
-//   pass 1: recompute the scores and write exp(s - max) / sum once.
+// Work decomposition.  One workgroup = 256 rows of one batch (8 waves x 2 x 16
+// rows); it streams the N axis in 64-column tiles of rhs^T (two fp16 limb
+// planes [N][K] and the tile scales, made by split_transpose_kernel), DMA'd
+// global->LDS into a ring of three buffers shared by the 8 waves.  Two passes
+// over N:
+//   pass 0: online row max and sum of 2^(s - max) (flash-softmax statistics);
+//   pass 1: recompute the scores and write 2^(s - max) / sum once.
 // The output (4 bytes per element) is written exactly once; recomputing the
-// K = 64 scores is cheaper than a second pass over the output in HBM.
+// K = 64 scores is cheaper than a second pass over the output in HBM.  Scores
+// are kept in log2 units (lhs is multiplied by log2(e) before the split), so
+// each exponential is one v_exp_f32.
 //
-// Per wave and 64-column tile: the MFMA B operand is the 16-row block of lhs
+// Per wave and 64-column tile: the MFMA B operand is a 16-row block of lhs
 // (held in registers for the whole kernel, split on load), the MFMA A operand a
 // 16-column block of rhs^T read from LDS (ds_read_b128, 128-byte rows, chunk c of
 // row r at c ^ (r & 7)); lane l then holds row l % 16, columns 4*(l/16) .. +3 of
@@ -28,57 +36,83 @@
 #include <math.h>
 
 #include "common.h"
+#include "lanes.h"
 
 namespace kda {
 namespace bmmsm {
 
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kRows = 16 * kWaves;   // rows per workgroup
-constexpr int kCols = 64;            // columns per tile
-constexpr int kK = 64;               // max contraction (two 32-wide MFMA k steps)
-constexpr int kLimbs = 3;
+constexpr int kGroups = 2;                       // 16-row groups per wave
+constexpr int kRows = 16 * kGroups * kWaves;     // 256 rows per workgroup
+constexpr int kCols = 64;                        // columns per tile
+constexpr int kK = 64;                           // max contraction (two 32-wide MFMA k steps)
+constexpr int kLimbs = 2;
 constexpr int kXcds = 8;
-constexpr int kPlaneBytes = kCols * kK * 2;           // one limb plane of a tile
-constexpr int kTileBytes = kLimbs * kPlaneBytes;      // 24 KiB
-constexpr int kDmaPerWave = kTileBytes / 1024 / kWaves;   // 3
-constexpr int kStages = 3;                               // tile ring depth
-constexpr int kStoresPerTile = 4;                        // store instructions per wave
+constexpr int kPlaneBytes = kCols * kK * 2;               // one limb plane of a tile
+constexpr int kTileBytes = kLimbs * kPlaneBytes;          // 16 KiB
+constexpr int kDmaPerWave = kTileBytes / 1024 / kWaves;   // 2
+constexpr int kStages = 3;                                // tile ring depth
+constexpr int kStores = 4 * kGroups;                      // store instructions per wave and tile
+constexpr int kTopExp = 13;                               // largest |scaled value| in [2^13, 2^14)
+constexpr float kLog2e = 1.44269504088896341f;
 #define KDA_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
-__device__ __forceinline__ void limbs3(float x, uint32_t& b0, uint32_t& b1, uint32_t& b2) {
-  b0 = f32_to_bf16_bits(x);
-  const float r1 = x - bf16_bits_to_f32(b0);
-  b1 = f32_to_bf16_bits(r1);
-  const float r2 = r1 - bf16_bits_to_f32(b1);
-  b2 = f32_to_bf16_bits(r2);
+// 2^e for e in [-126, 127], from the exponent bits.
+__device__ __forceinline__ float pow2(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
+
+// Exponent of a non-negative float's leading bit, clamped to [-100, 128] so that
+// both 2^(kTopExp - e) and 2^(e - kTopExp) stay normal (0 gives -100; inf and
+// NaN give 128 and stay non-finite after scaling).
+__device__ __forceinline__ int top_exponent(float mx) {
+  return max((int)((__float_as_uint(mx) >> 23) & 0xff) - 127, -100);
 }
 
-// rhs [B][K][N] fp32 -> three bf16 limb planes of rhs^T, each [B][N][64] (k
-// padded with zeros up to 64).  One workgroup per (64-column block, batch).
+// Two fp16 limbs of x (|x| < 2^14 + rounding): x0 = fp16(x), x1 = fp16(x - x0);
+// x - x0 is exact in fp32.
+__device__ __forceinline__ void limbs2(float x, _Float16& h0, _Float16& h1) {
+  h0 = (_Float16)x;
+  h1 = (_Float16)(x - (float)h0);
+}
+
+// rhs [B][K][N] fp32 -> two fp16 limb planes of rhs^T * 2^(kTopExp - e), each
+// [B][N][64] (k padded with zeros up to 64), and tile_scale[b][tile] =
+// 2^(e - kTopExp), where 2^e is the leading power of two of the tile's largest
+// |value|.  One workgroup per (64-column tile, batch).
 __global__ __launch_bounds__(256) void split_transpose_kernel(const float* __restrict__ rhs,
-                                                              uint16_t* __restrict__ p0,
-                                                              uint16_t* __restrict__ p1,
-                                                              uint16_t* __restrict__ p2, int k,
+                                                              _Float16* __restrict__ p0,
+                                                              _Float16* __restrict__ p1,
+                                                              float* __restrict__ tile_scale, int k,
                                                               int n) {
   __shared__ float tile[kK][kCols + 1];
+  __shared__ float wave_max[4];
   const int n0 = blockIdx.x * kCols;
   const int64_t b = blockIdx.y;
   const float* src = rhs + b * (int64_t)k * n;
+  float mx = 0.f;
   for (int idx = threadIdx.x; idx < kK * kCols; idx += 256) {
     const int r = idx / kCols, c = idx % kCols;   // r = k, c = column (coalesced read)
-    tile[r][c] = r < k ? src[(int64_t)r * n + n0 + c] : 0.f;
+    const float v = r < k ? src[(int64_t)r * n + n0 + c] : 0.f;
+    tile[r][c] = v;
+    mx = fmaxf(mx, fabsf(v));
   }
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x >> 6] = mx;
   __syncthreads();
+  mx = fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3]));
+  const int e = top_exponent(mx);
+  const float sc = pow2(kTopExp - e);
+  if (threadIdx.x == 0) tile_scale[b * (n / kCols) + blockIdx.x] = pow2(e - kTopExp);
   const int64_t base = (b * n + n0) * kK;
   for (int idx = threadIdx.x; idx < kK * kCols; idx += 256) {
     const int c = idx / kK, r = idx % kK;         // write k-contiguous
-    uint32_t h0, h1, h2;
-    limbs3(tile[r][c], h0, h1, h2);
+    _Float16 h0, h1;
+    limbs2(tile[r][c] * sc, h0, h1);
     const int64_t o = base + (int64_t)c * kK + r;
-    p0[o] = (uint16_t)h0;
-    p1[o] = (uint16_t)h1;
-    p2[o] = (uint16_t)h2;
+    p0[o] = h0;
+    p1[o] = h1;
   }
 }
 
@@ -93,24 +127,41 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-__global__ __launch_bounds__(kThreads, 2) void bmm_softmax_kernel(
-    const float* __restrict__ lhs, const uint16_t* __restrict__ p0, const uint16_t* __restrict__ p1,
-    const uint16_t* __restrict__ p2, float* __restrict__ out, int m, int n, int k) {
+// Scaled scores of one 64-column tile for the wave's kGroups x 16 rows:
+// s[g][j] lane l = rows 16g + l%16, columns 16j + 4(l/16) .. +3.  The score in
+// log2 units is s * row_scale[g] * tile_scale.
+using Scores = floatx4[kGroups][4];
+
+// Orders the MFMAs of the next tile between the VALU / transcendental work of
+// the current one (N MFMA slots, V vector instructions after each).
+template <int N, int V>
+__device__ __forceinline__ void interleave() {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x402, V, 0);   // VALU | TRANS
+  }
+}
+
+__global__ __launch_bounds__(kThreads, 1) void bmm_softmax_kernel(
+    const float* __restrict__ lhs, const _Float16* __restrict__ p0, const _Float16* __restrict__ p1,
+    const float* __restrict__ tile_scale, float* __restrict__ out, int m, int n, int k) {
   __shared__ __align__(1024) uint8_t lds[kStages][kTileBytes];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // Workgroups are dealt round-robin to the 8 XCDs; remap the linear id so each
   // XCD gets a contiguous range of (batch, row block) pairs.  All workgroups of
   // a batch then share one L2, which holds that batch's rhs limb planes
-  // (1.5 MiB at N = 4096) for the two passes of every row block.
+  // (1 MiB at N = 4096) for the two passes of every row block.
   const int row_blocks = (m + kRows - 1) / kRows;
   const int total_wg = row_blocks * (int)gridDim.y;
   int pid = blockIdx.y * row_blocks + blockIdx.x;
   const int full = (total_wg / kXcds) * kXcds;
   if (pid < full) pid = (pid % kXcds) * (full / kXcds) + pid / kXcds;
   const int64_t b = pid / row_blocks;
-  const int row0 = (pid % row_blocks) * kRows + wave * 16;
+  const int row0 = (pid % row_blocks) * kRows + wave * (16 * kGroups);
   const int nt = n / kCols;
+  const float* tscale = tile_scale + b * nt;
   // Column tiles are visited in a per-workgroup rotated order.  In pass 1 every
   // workgroup writes 256 bytes of each of its rows per tile; with all
   // workgroups on the same column tile the concurrent stores share their low
@@ -118,168 +169,219 @@ __global__ __launch_bounds__(kThreads, 2) void bmm_softmax_kernel(
   // (measured 20% slower at 16x4096x4096).
   const int rot = (int)((pid * (int64_t)7) % nt);
 
-  // ---- this wave's 16 rows of lhs as MFMA "B" fragments, split into 3 limbs:
-  // lane l holds row row0 + l%16, k = kh*32 + 8*(l/16) .. +7
-  bf16x8 a[2][kLimbs];
-  {
-    const int r = min(row0 + (lane & 15), m - 1);
+  // ---- the wave's rows of lhs * log2(e), scaled per row, as MFMA "B" fragments
+  // in two fp16 limbs: lane l holds row row0 + 16g + l%16, k = kh*32 + 8*(l/16) .. +7.
+  // Rows beyond m are clamped to m-1: those lanes recompute row m-1 bit for bit
+  // and store the same values into it, which keeps every store unconditional.
+  half8 a[kGroups][2][kLimbs];
+  float row_scale[kGroups];
+  float* orow[kGroups];
+#pragma unroll
+  for (int g = 0; g < kGroups; ++g) {
+    const int r = min(row0 + 16 * g + (lane & 15), m - 1);
     const float* src = lhs + (b * m + r) * (int64_t)k;
+    orow[g] = out + (b * m + r) * (int64_t)n + 4 * (lane >> 4);
+    float v[2][8];
+    float mx = 0.f;
 #pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-      const int kk = kh * 32 + 8 * (lane >> 4);
-      float v[8];
+    for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (kk + e < k) ? src[kk + e] : 0.f;
-      uint32_t w0[4], w1[4], w2[4];
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        uint32_t x0, x1, x2, y0, y1, y2;
-        limbs3(v[e], x0, x1, x2);
-        limbs3(v[e + 1], y0, y1, y2);
-        w0[e / 2] = x0 | (y0 << 16);
-        w1[e / 2] = x1 | (y1 << 16);
-        w2[e / 2] = x2 | (y2 << 16);
+      for (int e = 0; e < 8; ++e) {
+        const int kk = kh * 32 + 8 * (lane >> 4) + e;
+        v[kh][e] = kk < k ? src[kk] * kLog2e : 0.f;
+        mx = fmaxf(mx, fabsf(v[kh][e]));
       }
-      a[kh][0] = __builtin_bit_cast(bf16x8, (u32x4{w0[0], w0[1], w0[2], w0[3]}));
-      a[kh][1] = __builtin_bit_cast(bf16x8, (u32x4{w1[0], w1[1], w1[2], w1[3]}));
-      a[kh][2] = __builtin_bit_cast(bf16x8, (u32x4{w2[0], w2[1], w2[2], w2[3]}));
-    }
+    const int ex = top_exponent(row_max4(mx));
+    const float sc = pow2(kTopExp - ex);
+    row_scale[g] = pow2(ex - kTopExp);
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        _Float16 h0, h1;
+        limbs2(v[kh][e] * sc, h0, h1);
+        a[g][kh][0][e] = h0;
+        a[g][kh][1][e] = h1;
+      }
   }
 
-  // ---- DMA of column tile t (of the N axis) into buffer `buf`: 24 x 1 KiB
-  // instructions, 3 per wave; instruction q fills plane q/8, rows (q%8)*8 ..+7
+  // ---- DMA of column tile c (of the N axis) into buffer `buf`: 16 x 1 KiB
+  // instructions, 2 per wave; instruction q fills plane q/8, rows (q%8)*8 ..+7
   // (8 lanes per 128-byte row, chunk c of row r stored at c ^ (r & 7)).
-  const uint16_t* planes[kLimbs] = {p0, p1, p2};
+  const _Float16* planes[kLimbs] = {p0, p1};
   const uint32_t lds_base = (uint32_t)(uintptr_t)KDA_LDS_PTR(&lds[0][0]);
-  auto issue = [&](int t, int buf) {
-    const int c0 = t * kCols;
+  auto issue = [&](int c, int buf) {
+    const int c0 = c * kCols;
 #pragma unroll
     for (int j = 0; j < kDmaPerWave; ++j) {
       const int q = j * kWaves + wave;
       const int plane = q / 8, qq = q % 8;
       const int r = qq * 8 + lane / 8;
       const int chunk = (lane % 8) ^ (r & 7);
-      const uint16_t* src = planes[plane] + ((b * n + c0 + r) * kK + chunk * 8);
+      const _Float16* src = planes[plane] + ((b * n + c0 + r) * kK + chunk * 8);
       dma16(src, lds_base + buf * kTileBytes + plane * kPlaneBytes + qq * 1024);
     }
   };
 
-  // Scores of the 64-column tile in buffer `buf`: 4 independent 16x16 blocks,
-  // issued term by term so consecutive MFMAs never depend on each other.
-  auto scores = [&](int buf, floatx4 (&s)[4]) {
+  // Scores of the tile in buffer `buf`: 2 x 4 independent 16x16 blocks, issued
+  // term by term so consecutive MFMAs never depend on each other.
+  auto scores = [&](int buf, Scores& s) {
     const uint8_t* tile = &lds[buf][0];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) s[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int g = 0; g < kGroups; ++g)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s[g][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
       const int c = kh * 4 + (lane >> 4);
-      bf16x8 bt[4][kLimbs];
+      half8 bt[4][kLimbs];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = j * 16 + (lane & 15);
 #pragma unroll
         for (int l = 0; l < kLimbs; ++l)
-          bt[j][l] = *reinterpret_cast<const bf16x8*>(tile + l * kPlaneBytes + r * 128 + ((c ^ (r & 7)) << 4));
+          bt[j][l] = *reinterpret_cast<const half8*>(tile + l * kPlaneBytes + r * 128 + ((c ^ (r & 7)) << 4));
       }
-      // smallest terms first: (2,0) (1,1) (0,2) (1,0) (0,1) (0,0)
-      constexpr int kTerm[6][2] = {{0, 2}, {1, 1}, {2, 0}, {0, 1}, {1, 0}, {0, 0}};
+      // smaller terms first: (1,0) (0,1) (0,0)
+      constexpr int kTerm[3][2] = {{0, 1}, {1, 0}, {0, 0}};
 #pragma unroll
-      for (int t = 0; t < 6; ++t)
+      for (int t = 0; t < 3; ++t)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bt[j][kTerm[t][0]], a[kh][kTerm[t][1]], s[j],
-                                                         0, 0, 0);
+        for (int g = 0; g < kGroups; ++g)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            s[g][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bt[j][kTerm[t][0]], a[g][kh][kTerm[t][1]],
+                                                             s[g][j], 0, 0, 0);
     }
   };
 
-  // Software pipeline per tile t (ring of kStages LDS buffers):
-  //   wait for this wave's DMA of tile t, barrier (tile t visible everywhere,
-  //   buffer (t-1) % kStages free), issue the DMA of tile t+2, store the
-  //   probabilities of tile t-1, compute tile t.
-  // vmcnt counts loads and stores together and retires in issue order, so the
-  // wait for DMA(t) lets the operations issued after it stay in flight: the
-  // stores of iteration t-2 and the DMA and stores of iteration t-1.  Stores
-  // of the output therefore overlap two further tiles of compute.
-  const int total = 2 * nt;   // tiles over both passes
-  issue(rot, 0);
-  if (total > 1) issue((1 + rot) % nt, 1);
-  float m_run = -INFINITY, l_run = 0.f, inv_l = 0.f;
-  const int grow = row0 + (lane & 15);
-  const bool row_ok = grow < m;
-  const bool wave_rows = row0 < m;   // wave-uniform: the wave owns a valid row
-  float* orow = out + (b * m + min(grow, m - 1)) * (int64_t)n + 4 * (lane >> 4);
-  floatx4 pend[4];            // probabilities of the previous tile (pass 1)
-  int pend_col = -1;          // its first column, or -1
-  // Returns the number of store instructions issued (wave-uniform).
-  auto flush = [&]() -> int {
-    int issued = 0;
-    if (pend_col >= 0 && wave_rows) {
-      if (row_ok) {
-        // plain stores: each instruction writes 16 rows x 64 bytes; L2 merges
-        // the halves of each 128-byte line (non-temporal 64-byte pieces
-        // measured at 3.4 TB/s against 5.5 TB/s for plain stores)
+  // pass 0: online row statistics (max, and sum of 2^(s - max) per lane)
+  float m_run[kGroups], l_run[kGroups], inv_l[kGroups];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          *reinterpret_cast<floatx4*>(orow + pend_col + j * 16) = pend[j];
-      }
-      issued = kStoresPerTile;   // lane 0's row is valid, so the exec mask is non-empty
-    }
-    pend_col = -1;
-    return issued;
-  };
-  int st_prev2 = 0, st_prev1 = 0;   // stores issued by iterations t-2 and t-1
-  for (int t = 0; t < total; ++t) {
-    const int buf = t % kStages;
-    // in flight after DMA(t): stores(t-2), DMA(t+1), stores(t-1)
-    const int after = st_prev2 + (t + 1 < total ? kDmaPerWave : 0) + st_prev1;
-    switch (after) {
-      case 11: wait_vmcnt<11>(); break;
-      case 8: wait_vmcnt<8>(); break;
-      case 7: wait_vmcnt<7>(); break;
-      case 4: wait_vmcnt<4>(); break;
-      case 3: wait_vmcnt<3>(); break;
-      default: wait_vmcnt<0>(); break;
-    }
-    __builtin_amdgcn_s_barrier();   // tile t visible; buffer (t-1) % kStages free
-    asm volatile("" ::: "memory");
-    if (t + 2 < total) issue((t + 2 + rot) % nt, (t + 2) % kStages);
-    st_prev2 = st_prev1;
-    st_prev1 = flush();
-    floatx4 s[4];
-    scores(buf, s);
-    if (t < nt) {
-      // pass 0: online statistics; the 4 lanes l, l+16, l+32, l+48 share a row
-      float mx = -INFINITY;
+  for (int g = 0; g < kGroups; ++g) m_run[g] = -INFINITY, l_run[g] = 0.f;
+  auto stats = [&](const Scores& s, float ts) {
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+      const float c = row_scale[g] * ts;
+      float mx = s[g][0][0];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[j][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run, mx);
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[g][j][r]);
+      const float m_new = fmaxf(m_run[g], row_max4(mx) * c);
       float sum = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sum += __expf(s[j][r] - m_new);
-      l_run = l_run * __expf(m_run - m_new) + sum;
-      m_run = m_new;
-      if (t + 1 == nt) {
-        float l = l_run;
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
-        inv_l = 1.0f / l;
-      }
-    } else {
-      // pass 1: normalised probabilities, written once (next iteration)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) pend[j][r] = __expf(s[j][r] - m_run) * inv_l;
-      pend_col = ((t - nt + rot) % nt) * kCols;
+        for (int r = 0; r < 4; ++r) sum += __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][j][r], c, -m_new));
+      l_run[g] = l_run[g] * __builtin_amdgcn_exp2f(m_run[g] - m_new) + sum;
+      m_run[g] = m_new;
     }
+  };
+  // pass 1: normalised probabilities of column tile col, stored directly
+  auto probs = [&](const Scores& s, float ts, int col) {
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+      const float c = row_scale[g] * ts;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        floatx4 p;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][j][r], c, -m_run[g])) * inv_l[g];
+        *reinterpret_cast<floatx4*>(orow[g] + col * kCols + j * 16) = p;
+      }
+    }
+  };
+
+  // Software pipeline over the 2*nt steps (step t = column tile (t + rot) % nt,
+  // pass t / nt), ring of kStages LDS buffers.  Iteration t: wait for this
+  // wave's DMA of step t+1, barrier (step t+1 visible everywhere; buffer t %
+  // kStages, last read by the MFMAs of step t one iteration ago, is free), issue
+  // the DMA of step t+3 into it, then the MFMAs of step t+1 interleaved with the
+  // softmax work of step t, whose scores the previous iteration produced.
+  // vmcnt counts loads and stores together and retires in issue order: after
+  // DMA(t+1) come the stores of iteration t-2, DMA(t+2) and the stores of
+  // iteration t-1, which may stay in flight.
+  const int total = 2 * nt;
+  auto col = [&](int t) { return (t + rot) % nt; };
+  auto dma_after = [&](int t) {   // operations allowed in flight at iteration t
+    return (t - 2 >= nt ? kStores : 0) + (t + 2 < total ? kDmaPerWave : 0) + (t - 1 >= nt ? kStores : 0);
+  };
+  auto wait_step = [&](int t) {
+    switch (dma_after(t)) {
+      case 2 * kStores + kDmaPerWave: wait_vmcnt<2 * kStores + kDmaPerWave>(); break;
+      case 2 * kStores: wait_vmcnt<2 * kStores>(); break;
+      case kStores + kDmaPerWave: wait_vmcnt<kStores + kDmaPerWave>(); break;
+      case kStores: wait_vmcnt<kStores>(); break;
+      case kDmaPerWave: wait_vmcnt<kDmaPerWave>(); break;
+      default: wait_vmcnt<0>(); break;
+    }
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (t + 3 < total) issue(col(t + 3), (t + 3) % kStages);
+  };
+
+  issue(col(0), 0);
+  issue(col(1), 1);   // total >= 2
+  if (total > 2) {
+    issue(col(2), 2);
+    wait_vmcnt<2 * kDmaPerWave>();
+  } else {
+    wait_vmcnt<kDmaPerWave>();
   }
-  flush();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  Scores sa, sb;
+  scores(0, sa);
+  float ta = tscale[col(0)], tb;
+
+  // one pipeline iteration; `cur` / `ts` hold step t, `next` / `ts_next`
+  // receive step t+1
+  auto step0 = [&](int t, const Scores& cur, float ts, Scores& next, float& ts_next) {
+    wait_step(t);
+    ts_next = tscale[col(t + 1)];
+    scores((t + 1) % kStages, next);
+    stats(cur, ts);
+    interleave<48, 2>();
+    // keep the statistics in this block: without a use here LLVM sinks them
+    // past the next wait's branches, away from the MFMAs they should overlap
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) asm volatile("" ::"v"(m_run[g]), "v"(l_run[g]));
+  };
+  auto step1 = [&](int t, const Scores& cur, float ts, Scores& next, float& ts_next) {
+    wait_step(t);
+    ts_next = tscale[col(t + 1)];
+    scores((t + 1) % kStages, next);
+    probs(cur, ts, col(t));
+    interleave<48, 2>();
+  };
+  int t = 0;
+  for (; t + 1 < nt; t += 2) {
+    step0(t, sa, ta, sb, tb);
+    step0(t + 1, sb, tb, sa, ta);
+  }
+  if (t < nt) {   // odd nt: one more statistics step, then bring its output to sa
+    step0(t, sa, ta, sb, tb);
+    ++t;
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sa[g][j] = sb[g][j];
+    ta = tb;
+  }
+#pragma unroll
+  for (int g = 0; g < kGroups; ++g) inv_l[g] = 1.0f / row_sum4(l_run[g]);
+  for (; t + 1 < total - 1; t += 2) {
+    step1(t, sa, ta, sb, tb);
+    step1(t + 1, sb, tb, sa, ta);
+  }
+  if (t < total - 1) {
+    step1(t, sa, ta, sb, tb);
+    probs(sb, tb, col(t + 1));
+  } else {
+    probs(sa, ta, col(t));
+  }
 }
 
 }  // namespace bmmsm
@@ -312,13 +414,13 @@ extern "C" int kda_bmm_softmax_f32(const float* lhs, const float* rhs, float* ou
                      what, (long long)need);
   hipStream_t st = as_stream(stream);
   const int64_t plane = batch * n * kK;   // elements per limb plane
-  uint16_t* q0 = reinterpret_cast<uint16_t*>(workspace);
-  uint16_t* q1 = q0 + plane;
-  uint16_t* q2 = q1 + plane;
+  _Float16* q0 = reinterpret_cast<_Float16*>(workspace);
+  _Float16* q1 = q0 + plane;
+  float* tscale = reinterpret_cast<float*>(q1 + plane);   // [B][N/64]
   hipLaunchKernelGGL(split_transpose_kernel, dim3((unsigned)(n / kCols), (unsigned)batch), dim3(256),
-                     0, st, rhs, q0, q1, q2, (int)k, (int)n);
+                     0, st, rhs, q0, q1, tscale, (int)k, (int)n);
   if (int rc = check_launch(what)) return rc;
   hipLaunchKernelGGL(bmm_softmax_kernel, dim3((unsigned)((m + kRows - 1) / kRows), (unsigned)batch),
-                     dim3(kThreads), 0, st, lhs, q0, q1, q2, out, (int)m, (int)n, (int)k);
+                     dim3(kThreads), 0, st, lhs, q0, q1, tscale, out, (int)m, (int)n, (int)k);
   return check_launch(what);
 }

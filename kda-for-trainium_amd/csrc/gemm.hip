@@ -939,8 +939,8 @@ int64_t workspace_bytes(int op, int64_t b, int64_t m, int64_t k, int64_t n, int6
     case KDA_OP_RMSNORM_MATMUL_BF16:
       plan_rms_bf16(c, m, k);
       break;
-    case KDA_OP_BMM_SOFTMAX_F32:   // three bf16 limb planes of rhs^T, [B][N][64] each
-      c.take<uint16_t>(3 * b * n * 64);
+    case KDA_OP_BMM_SOFTMAX_F32:   // two fp16 limb planes of rhs^T [B][N][64], tile scales [B][N/64]
+      c.take<uint16_t>(2 * b * n * 64 + 2 * b * ((n + 63) / 64));
       break;
     default:
       return -1;
