@@ -145,6 +145,9 @@ NKIBENCH = {
     "bmm_softmax": dict(desc="softmax([16,4096,64]@[16,64,4096], -1)", dims=dict(B=16, M=4096, K=64, N=4096),
                         bound="hbm",
                         work=4 * (2 * 16 * 4096 * 64 + 16 * 4096 * 4096)),
+    "gqa_full": dict(desc="q[1,4096,16,128] k,v[1,4096,8,128] fp32, non-causal, BHSD out",
+                     dims=dict(B=1, S=4096, HQ=16, HKV=8, D=128), bound="mfma",
+                     useful=4 * 16 * 4096 * 4096 * 128, work=3 * 4 * 16 * 4096 * 4096 * 128),
 }
 
 
@@ -176,6 +179,8 @@ def make_nki_case(name, dev, seed=0):
         sets = draw(2, std=0.05)
         return (lambda i: ops.mamba(*sets[i % 2])), sets
     (args,) = draw(1)
+    if name == "gqa_full":
+        return (lambda i: ops.gqa(*args, causal=False, out_layout="bhsd")), args
     fn = getattr(ops, name)
     if name in ("add_rmsnorm_matmul", "matmul_add_rmsnorm"):
         x, w, z, gg = args
@@ -212,12 +217,16 @@ def _nki_shapes(name, d):
     if name == "swiglu":
         M, K, N = d["M"], d["K"], d["N"]
         return [(M, K), (K, N), (N, K), (K, N)]
+    if name == "gqa_full":
+        B, S, D = d["B"], d["S"], d["D"]
+        return [(B, S, d["HQ"], D), (B, S, d["HKV"], D), (B, S, d["HKV"], D)]
     raise KeyError(name)
 
 
 def nki_cpu_baseline(name, reps=3):
     """The oracle (numpy) forward of an NKIBench op on this host; bmm_softmax and
-    bmm on 2 of the 16 batches, scaled x8.  Returns (ms, sample description)."""
+    bmm on 2 of the 16 batches, gqa_full on 2 of the 16 query heads, scaled x8.
+    Returns (ms, sample description)."""
     import numpy as np
     from oracle import inputs as oi
     from oracle import ops as oo
@@ -226,7 +235,11 @@ def nki_cpu_baseline(name, reps=3):
     if name in ("bmm", "bmm_softmax"):
         dims, scale = dict(B=2), 8
     d = oi.draw(name, 0, dims=dims)
-    fn = getattr(oo, name)
+    if name == "gqa_full":
+        scale = 8
+        fn = lambda **kw: oo.gqa(**kw, heads=[(0, 0), (0, 1)])
+    else:
+        fn = getattr(oo, name)
     fn(**d)
     ts = []
     for _ in range(reps):
@@ -234,7 +247,8 @@ def nki_cpu_baseline(name, reps=3):
         fn(**d)
         ts.append(time.perf_counter() - t0)
     ms = sorted(ts)[len(ts) // 2] * 1e3 * scale
-    return ms, ("full shape" if scale == 1 else f"2 of 16 batches, scaled x{scale}")
+    what = "heads" if name == "gqa_full" else "batches"
+    return ms, ("full shape" if scale == 1 else f"2 of 16 {what}, scaled x{scale}")
 
 
 # ----------------------------------------------------------------- CPU baseline

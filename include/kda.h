@@ -88,7 +88,8 @@ enum {
   KDA_OP_MATMUL_ADD_RMSNORM_F32 = 7,
   KDA_OP_SWIGLU_F32 = 8,          /* n = F (intermediate width) */
   KDA_OP_RMSNORM_MATMUL_BF16 = 9,
-  KDA_OP_BMM_SOFTMAX_F32 = 10
+  KDA_OP_BMM_SOFTMAX_F32 = 10,
+  KDA_OP_GQA_F32 = 11             /* batch = B, m = S, k = Hq, n = Hkv */
 };
 
 /* Workspace bytes for operator `op` at the given sizes (unused sizes: 0);
@@ -222,6 +223,19 @@ int kda_gqa_fwd_bf16(const kda_bf16* q, const kda_bf16* k, const kda_bf16* v, kd
                      int64_t batch, int64_t seq, int64_t hq, int64_t hkv, int64_t head_dim,
                      float scale, int causal, int64_t out_stride_b, int64_t out_stride_s,
                      int64_t out_stride_h, void* stream);
+
+/* The same attention for fp32 q/k/v/out with fp32-class accuracy: q, k and v are
+ * scaled by powers of two (q per row, k per 64-key tile, v per kv head) and split
+ * into two fp16 limbs; QK^T and PV each take three fp16 MFMA products (~22
+ * significant bits).  G = Hq/Hkv must be 2 and D 128; output strides as above.
+ * Workspace: KDA_OP_GQA_F32 (limb planes and scales).
+ * Replaces kernel(v1=q, v2=k, v3=v) of
+ * workspaces/gqa_full/runs/gqa_full_v7a_exp_from_psum.py:15-220 at its own fp32
+ * inputs (B1 S4096 Hq16 Hkv8 D128, non-causal, BHSD out). */
+int kda_gqa_fwd_f32(const float* q, const float* k, const float* v, float* out, int64_t batch,
+                    int64_t seq, int64_t hq, int64_t hkv, int64_t head_dim, float scale,
+                    int causal, int64_t out_stride_b, int64_t out_stride_s, int64_t out_stride_h,
+                    void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

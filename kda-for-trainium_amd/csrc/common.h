@@ -30,6 +30,9 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // Number of compute units on the current device (cached per device).
 int device_cu_count();
 
+// Workspace bytes of kda_gqa_fwd_f32 (layout owned by attention_f32.hip).
+int64_t gqa_f32_workspace_bytes(int64_t batch, int64_t seq, int64_t hq, int64_t hkv);
+
 // ---- device helpers -------------------------------------------------------
 
 // fp32 -> bf16 bits, round to nearest even (finite inputs; NaN stays NaN).

@@ -942,6 +942,8 @@ int64_t workspace_bytes(int op, int64_t b, int64_t m, int64_t k, int64_t n, int6
     case KDA_OP_BMM_SOFTMAX_F32:   // two fp16 limb planes of rhs^T [B][N][64], tile scales [B][N/64]
       c.take<uint16_t>(2 * b * n * 64 + 2 * b * ((n + 63) / 64));
       break;
+    case KDA_OP_GQA_F32:           // m = S, k = Hq, n = Hkv
+      return gqa_f32_workspace_bytes(b, m, k, n);
     default:
       return -1;
   }

@@ -441,9 +441,15 @@ def mamba(delta: torch.Tensor, u: torch.Tensor, a: torch.Tensor, b: torch.Tensor
 # ----------------------------------------------------------------- attention
 
 def gqa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False,
-        scale: Optional[float] = None, out_layout: str = "bshd") -> torch.Tensor:
+        scale: Optional[float] = None, out_layout: str = "bshd",
+        workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Grouped-query softmax attention: per query head h (kv head h // (Hq/Hkv)),
     ``softmax(q k^T * scale) v`` with an fp32 online softmax (flash style).
+
+    bf16 q/k/v (4 query heads per kv head) run on bf16 MFMA and return bf16; fp32
+    q/k/v (2 query heads per kv head, the reference's gqa_full case) run on a
+    two-limb fp16 split with fp32-class accuracy and return fp32 (workspace:
+    KDA_OP_GQA_F32 bytes, allocated when not given).
 
     q (B, S, Hq, D), k/v (B, S, Hkv, D); scale defaults to 1/sqrt(D); causal masks
     keys after the query.  out_layout "bshd" returns (B, S, Hq, D); "bhsd" returns
@@ -462,16 +468,22 @@ def gqa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False,
     if hq % hkv:
         raise ValueError(f"gqa: Hq={hq} is not a multiple of Hkv={hkv}")
     sc = (1.0 / math.sqrt(d)) if scale is None else float(scale)
-    if q.dtype != BF16:
+    if q.dtype not in (BF16, F32):
         raise ValueError(f"gqa: unsupported dtype {q.dtype}")
     if out_layout == "bshd":
-        out = torch.empty((bsz, s, hq, d), dtype=BF16, device=q.device)
+        out = torch.empty((bsz, s, hq, d), dtype=q.dtype, device=q.device)
         strides = (s * hq * d, hq * d, d)
     elif out_layout == "bhsd":
-        out = torch.empty((bsz, hq, s, d), dtype=BF16, device=q.device)
+        out = torch.empty((bsz, hq, s, d), dtype=q.dtype, device=q.device)
         strides = (hq * s * d, d, s * d)
     else:
         raise ValueError(f"gqa: out_layout must be 'bshd' or 'bhsd', got {out_layout!r}")
-    _lib.call("kda_gqa_fwd_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-              bsz, s, hq, hkv, d, sc, 1 if causal else 0, *strides, _stream(q))
+    if q.dtype == BF16:
+        _lib.call("kda_gqa_fwd_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                  bsz, s, hq, hkv, d, sc, 1 if causal else 0, *strides, _stream(q))
+        return out
+    ws = _workspace(workspace, workspace_size(_lib.OP_GQA_F32, bsz, s, hq, hkv), q.device)
+    _lib.call("kda_gqa_fwd_f32", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+              bsz, s, hq, hkv, d, sc, 1 if causal else 0, *strides, ws.data_ptr(), ws.numel(),
+              _stream(q))
     return out
