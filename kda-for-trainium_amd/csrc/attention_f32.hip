@@ -268,30 +268,25 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_f32_kernel(Args p) {
                        reinterpret_cast<const char*>(p.k1) + head_off};
   const char* vb[2] = {reinterpret_cast<const char*>(p.v0) + head_off,
                        reinterpret_cast<const char*>(p.v1) + head_off};
-  int drow[kDmaPerWave];
-  uint32_t kcol[kDmaPerWave], vcol[kDmaPerWave];
-#pragma unroll
-  for (int j = 0; j < kDmaPerWave; ++j) {
-    const int r = ((j & 1) * kWaves + wave) * 4 + (lane >> 4);
-    const int t = lane & 15;
-    drow[j] = r;
-    kcol[j] = (uint32_t)((t ^ kswz(r)) << 4);
-    vcol[j] = (uint32_t)(((((t >> 1) ^ mswz(r)) << 5)) + ((t & 1) << 4));
-  }
   auto k_tile = [&](int kt) { return smem + (kt & 1) * kTileBytes; };
   auto v_tile = [&](int kt) { return smem + (2 + (kt & 1)) * kTileBytes; };
   // Rows past the sequence are clamped to the last key: their scores are masked
-  // and their V rows meet p = 0.
+  // and their V rows meet p = 0.  (Addresses are recomputed per tile: a few
+  // VALU ops, against a dozen registers held across the loop.)
   auto issue = [&](int kt) {
     const int j0 = kt * kBN;
     const int last = p.seq - 1 - j0;
     const uint32_t kl = lds_addr(k_tile(kt)), vl = lds_addr(v_tile(kt));
+    const int t = lane & 15;
 #pragma unroll
     for (int j = 0; j < kDmaPerWave; ++j) {
-      const uint32_t roff = (uint32_t)(min(drow[j], last) * row_bytes);
+      const int r = ((j & 1) * kWaves + wave) * 4 + (lane >> 4);
+      const uint32_t roff = (uint32_t)(min(r, last) * row_bytes);
+      const uint32_t kcol = (uint32_t)((t ^ kswz(r)) << 4);
+      const uint32_t vcol = (uint32_t)((((t >> 1) ^ mswz(r)) << 5) + ((t & 1) << 4));
       const uint32_t dst = (uint32_t)((j * kWaves + wave) * 1024);
-      dma16(kb[j >> 1] + j0 * row_bytes, roff + kcol[j], kl + dst);
-      dma16(vb[j >> 1] + j0 * row_bytes, roff + vcol[j], vl + dst);
+      dma16(kb[j >> 1] + j0 * row_bytes, roff + kcol, kl + dst);
+      dma16(vb[j >> 1] + j0 * row_bytes, roff + vcol, vl + dst);
     }
   };
 
@@ -411,15 +406,21 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_f32_kernel(Args p) {
 
   // Iteration kt: wait for this wave's DMA of tile kt, barrier (tile kt visible;
   // slot (kt+1)&1, last read in iteration kt-1, is free), issue tile kt+1, compute.
+  // Two loops (unmasked tiles, then masked ones), one tile_step instance each:
+  // with both instances in one loop body the register allocator spills.
   issue(0);
-  for (int kt = 0; kt < nkt; ++kt) {
+  int kt = 0;
+  for (; kt < nfree; ++kt) {
     wait_vmcnt<0>();
     __syncthreads();
     if (kt + 1 < nkt) issue(kt + 1);
-    if (kt < nfree)
-      tile_step(std::false_type(), kt);
-    else
-      tile_step(std::true_type(), kt);
+    tile_step(std::false_type(), kt);
+  }
+  for (; kt < nkt; ++kt) {
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (kt + 1 < nkt) issue(kt + 1);
+    tile_step(std::true_type(), kt);
   }
 
   // ---- normalise and store: lane holds out[row][d = 16dt + 4g .. +3]
