@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import math
 import statistics
+import time
 from dataclasses import dataclass, field
 from typing import Any, Callable, Dict, List, Optional, Sequence
 
@@ -67,23 +68,34 @@ class Timing:
 
 
 def time_op(fn: Callable[[int], Any], warmup: int = 20, iters: int = 100,
-            device: Optional[torch.device] = None) -> Timing:
+            device: Optional[torch.device] = None, min_warmup_s: float = 0.2,
+            max_warmup: int = 4000) -> Timing:
     """Times ``fn(i)`` with HIP events on the current stream; returns p50/p10/p90.
 
     ``fn`` receives the iteration index so a caller can rotate through several
     input sets (memory-bound operators rotate more than the 256 MB Infinity
     Cache so repeated calls cannot be served from it).
+
+    Warm-up runs at least ``warmup`` calls and at least ``min_warmup_s`` seconds
+    of GPU time (at most ``max_warmup`` calls): after an idle spell the MI355X
+    needs tens of milliseconds of load to reach its steady clocks, and
+    sub-millisecond operators timed right after 10 calls read ~10% slow.
     """
     dev = device or torch.device("cuda", torch.cuda.current_device())
     stream = torch.cuda.current_stream(dev)
-    for i in range(warmup):
-        fn(i)
+    t0 = time.perf_counter()
+    done = 0
+    while done < warmup or (done < max_warmup and time.perf_counter() - t0 < min_warmup_s):
+        fn(done)
+        done += 1
+        if done % 8 == 0:
+            torch.cuda.synchronize(dev)
     torch.cuda.synchronize(dev)
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     for i in range(iters):
         starts[i].record(stream)
-        fn(warmup + i)
+        fn(done + i)
         ends[i].record(stream)
     torch.cuda.synchronize(dev)
     ms = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
