@@ -58,7 +58,7 @@ def make_gpu_case(name, dev, seed=0):
     """Synthetic inputs of each configuration's distribution, drawn on the GPU.
     Returns (fn(i) running one call on rotation slot i, keep-alive list)."""
     import torch
-    from kda import ops
+    from kda import _lib, ops
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     BF = torch.bfloat16
@@ -85,7 +85,9 @@ def make_gpu_case(name, dev, seed=0):
         wu = normal((4096, 14336), std=0.02, dtype=BF)
         wd = normal((14336, 4096), std=0.02, dtype=BF)
         h = torch.empty(2048, 14336, device=dev, dtype=BF)
-        return (lambda i: ops.swiglu(x, wu, wd, wg, h_workspace=h)), [x, wg, wu, wd, h]
+        ws = torch.empty(ops.workspace_size(_lib.OP_SWIGLU_BF16, 1, 2048, 4096, 14336), device=dev,
+                         dtype=torch.uint8)
+        return (lambda i: ops.swiglu(x, wu, wd, wg, h_workspace=h, workspace=ws)), [x, wg, wu, wd, h, ws]
     if name == "adamw":
         n = 1 << 27
         p, gr, m = normal((n,), std=0.02), normal((n,), std=1e-3), normal((n,), std=1e-4)

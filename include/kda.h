@@ -89,7 +89,8 @@ enum {
   KDA_OP_SWIGLU_F32 = 8,          /* n = F (intermediate width) */
   KDA_OP_RMSNORM_MATMUL_BF16 = 9,
   KDA_OP_BMM_SOFTMAX_F32 = 10,
-  KDA_OP_GQA_F32 = 11             /* batch = B, m = S, k = Hq, n = Hkv */
+  KDA_OP_GQA_F32 = 11,            /* batch = B, m = S, k = Hq, n = Hkv */
+  KDA_OP_SWIGLU_BF16 = 12         /* m = M, k = K: optional split-K partials */
 };
 
 /* Workspace bytes for operator `op` at the given sizes (unused sizes: 0);
@@ -118,11 +119,14 @@ int kda_rmsnorm_matmul_bf16(const kda_bf16* x, const kda_bf16* gamma, const kda_
 
 /* y[M,K] = (silu(x @ w_gate) * (x @ w_up)) @ w_down with x [M,K], w_up/w_gate [K,F],
  * w_down [F,K].  h is caller-provided scratch of M*F bf16 (the gated activation,
- * written by the first kernel and read by the second).  Argument order follows
+ * written by the first kernel and read by the second).  `workspace` (optional:
+ * NULL or too small disables it) of kda_workspace_size(KDA_OP_SWIGLU_BF16, 1, M,
+ * K, F, 0) bytes lets the down GEMM split F in two when its output tiles fill at
+ * most half the device (fp32 partials, summed into y).  Argument order follows
  * kernel(v1=x, v2=w_up, v3=w_down, v4=w_gate) of workspaces/swiglu/runs/swiglu_v1.py:38-146. */
 int kda_swiglu_bf16(const kda_bf16* x, const kda_bf16* w_up, const kda_bf16* w_down,
                     const kda_bf16* w_gate, kda_bf16* h, kda_bf16* y, int64_t m, int64_t k,
-                    int64_t f, void* stream);
+                    int64_t f, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------- fp32 GEMMs
  * The reference's fp32 NKIBench operators.  fp32 in, fp32 out, computed on bf16

@@ -41,7 +41,7 @@ SIGNATURES = {
     "kda_swiglu_f32": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
     "kda_bmm_softmax_f32": [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "kda_mamba_f32": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
-    "kda_swiglu_bf16": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
+    "kda_swiglu_bf16": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
     "kda_gqa_fwd_bf16": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _int,
                          _i64, _i64, _i64, _p],
     "kda_gqa_fwd_f32": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _int,
@@ -66,6 +66,7 @@ OP_SWIGLU_F32 = 8
 OP_RMSNORM_MATMUL_BF16 = 9
 OP_BMM_SOFTMAX_F32 = 10
 OP_GQA_F32 = 11
+OP_SWIGLU_BF16 = 12
 
 
 class KdaError(RuntimeError):

@@ -388,8 +388,9 @@ def swiglu(x: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor, w_gate: to
     kernel in workspaces/swiglu/runs/swiglu_v1.py:38-146).  bf16: the gated
     activation h (M, F) is produced by one fused dual-GEMM kernel (gate and up
     share each x tile; silu(gate)*up in the epilogue) and consumed by the down
-    GEMM; ``h_workspace`` optionally supplies h's (M, F) bf16 buffer.  fp32: the
-    same two kernels on split operands, h in fp32 (``workspace``).
+    GEMM; ``h_workspace`` optionally supplies h's (M, F) bf16 buffer and
+    ``workspace`` the down GEMM's split-K partials (KDA_OP_SWIGLU_BF16 bytes).
+    fp32: the same two kernels on split operands, h in fp32 (``workspace``).
     """
     dt = _same_dtype(("x", x), ("w_up", w_up), ("w_down", w_down), ("w_gate", w_gate))
     for name, t in (("w_up", w_up), ("w_down", w_down), ("w_gate", w_gate)):
@@ -407,8 +408,9 @@ def swiglu(x: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor, w_gate: to
     if h_workspace is None:
         h_workspace = torch.empty((m, f), dtype=BF16, device=x.device)
     _check("h_workspace", h_workspace, BF16, shape=(m, f))
+    ws = _workspace(workspace, workspace_size(_lib.OP_SWIGLU_BF16, 1, m, k, f), x.device)
     _lib.call("kda_swiglu_bf16", x.data_ptr(), w_up.data_ptr(), w_down.data_ptr(), w_gate.data_ptr(),
-              h_workspace.data_ptr(), out.data_ptr(), m, k, f, _stream(x))
+              h_workspace.data_ptr(), out.data_ptr(), m, k, f, ws.data_ptr(), ws.numel(), _stream(x))
     return out
 
 

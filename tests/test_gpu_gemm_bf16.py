@@ -85,6 +85,22 @@ def test_swiglu_config_full_size_all_seeds(dev):
         assert err < BF16_GATE
 
 
+def test_swiglu_config_without_split_k_workspace(dev):
+    # a workspace too small for the split-K partials: the down GEMM runs unsplit
+    d = oi.draw("swiglu_cfg", 1)
+    args = [to_dev(d[k], dev, BF) for k in ("x", "w_up", "w_down", "w_gate")]
+    tiny = torch.empty(16, dtype=torch.uint8, device=dev)
+    got = to_host(ops.swiglu(*args, workspace=tiny))
+    split = to_host(ops.swiglu(*args))
+    want = oo.swiglu(**d)
+    for name, out in (("unsplit", got), ("split", split)):
+        err = rel_l2(out, want)
+        print(f"swiglu_cfg {name} rel_l2={err:.3e}", flush=True)
+        assert err < BF16_GATE
+    # the two orders of the F sum differ by at most one bf16 rounding of the output
+    assert rel_l2(got, split) < 2.0 ** -8
+
+
 @pytest.mark.parametrize("dims", [dict(M=256, K=128, F=64), dict(M=50, K=96, F=200),
                                   dict(M=300, K=264, F=136)])
 def test_swiglu_ragged(dev, dims):
