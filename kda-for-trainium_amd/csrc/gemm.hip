@@ -74,6 +74,7 @@ enum class Epi {
   kStoreF32,       // fp32 C
   kSwiGLUF32,      // fp32 H = silu(acc_gate) * acc_up
   kAddZSsqF32,     // fp32 C = acc + z; part[m][n/64] = sum over the 64 columns of C^2
+  kStoreF32Pair,   // fp32 C = acc of B, C + c2_off = acc of B2 (two-B split-K partials)
 };
 
 // One K-segment: A_s (M x k), B_s (k x N) (and B2_s for two-B kernels).
@@ -94,6 +95,7 @@ struct Params {
   float* part;             // part[m*(N/64) + n/64]    (kAddZSsqF32)
   int64_t ldc;
   int64_t batch_a, batch_b, batch_c;   // per-batch strides (elements), batch = blockIdx.y
+  int64_t c2_off;          // offset of the second output (kStoreF32Pair), elements
   int m, n, k;             // k = sum of segment extents
 };
 
@@ -419,7 +421,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(Params p) {
         }
       }
       if (!ok) continue;
-      if constexpr (EPI == Epi::kStoreF32 || EPI == Epi::kSwiGLUF32 || EPI == Epi::kAddZSsqF32) {
+      if constexpr (EPI == Epi::kStoreF32Pair) {
+        *reinterpret_cast<floatx4*>(reinterpret_cast<float*>(p.c) + off) = acc[0][i][j];
+        *reinterpret_cast<floatx4*>(reinterpret_cast<float*>(p.c) + p.c2_off + off) = acc[NB - 1][i][j];
+      } else if constexpr (EPI == Epi::kStoreF32 || EPI == Epi::kSwiGLUF32 || EPI == Epi::kAddZSsqF32) {
         *reinterpret_cast<floatx4*>(reinterpret_cast<float*>(p.c) + off) =
             floatx4{v[0], v[1], v[2], v[3]};
       } else {
@@ -567,6 +572,22 @@ __global__ __launch_bounds__(256) void splitk2_bf16_kernel(const floatx4* __rest
     const floatx4 b = __builtin_nontemporal_load(part + n4 + i);
     const floatx4 v = a + b;
     y[i] = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  }
+}
+
+// SwiGLU columns computed as split-K partials part[s][q][M][F_tail] (s = k half,
+// q = 0 gate, 1 up): h[m][j] = bf16(silu(g) * u) with g, u the sums of the halves.
+__global__ __launch_bounds__(256) void swiglu_tail_kernel(const floatx4* __restrict__ part,
+                                                          uint16_t* __restrict__ h, int64_t m,
+                                                          int64_t ft, int64_t ldh) {
+  const int64_t n4 = m * ft / 4, q4 = n4;   // float4 per partial plane
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+    const floatx4 g = __builtin_nontemporal_load(part + i) + __builtin_nontemporal_load(part + 2 * q4 + i);
+    const floatx4 u = __builtin_nontemporal_load(part + q4 + i) + __builtin_nontemporal_load(part + 3 * q4 + i);
+    const int64_t row = (4 * i) / ft, col = (4 * i) % ft;
+    *reinterpret_cast<u32x2*>(h + row * ldh + col) =
+        u32x2{pack_bf16x2(silu_f(g[0]) * u[0], silu_f(g[1]) * u[1]),
+              pack_bf16x2(silu_f(g[2]) * u[2], silu_f(g[3]) * u[3])};
   }
 }
 
@@ -925,6 +946,23 @@ RmsBf16Plan plan_rms_bf16(Carve& c, int64_t m, int64_t k) {
   return p;
 }
 
+// SwiGLU gate/up GEMM on 256x128 tiles: when the tile count leaves a last, partly
+// idle round over the device and those r tiles are whole tile columns filling at
+// most half a round, the last f_tail = (r / tile rows) * 128 columns run as a
+// split-K pair (two launches' worth of half-K tiles in one round) into fp32
+// partials, and the rest in full rounds.
+struct UpSplit {
+  int64_t f_main, f_tail;
+};
+UpSplit plan_up(int64_t m, int64_t k, int64_t f) {
+  const int64_t cu = device_cu_count();
+  const int64_t tm = (m + 255) / 256, t = tm * ((f + 127) / 128), r = t % cu;
+  if (t <= cu || r == 0 || r % tm || 2 * r > cu || f % 128 || k % (2 * kBK))
+    return {f, 0};
+  const int64_t ft = (r / tm) * 128;
+  return {f - ft, ft};
+}
+
 int64_t workspace_bytes(int op, int64_t b, int64_t m, int64_t k, int64_t n, int64_t r) {
   Carve c{nullptr};
   switch (op) {
@@ -955,8 +993,8 @@ int64_t workspace_bytes(int op, int64_t b, int64_t m, int64_t k, int64_t n, int6
       break;
     case KDA_OP_GQA_F32:           // m = S, k = Hq, n = Hkv
       return gqa_f32_workspace_bytes(b, m, k, n);
-    case KDA_OP_SWIGLU_BF16:       // fp32 split-K partials of the down GEMM, [2][M][K]
-      c.take<float>(2 * m * k);
+    case KDA_OP_SWIGLU_BF16:       // fp32 split-K partials: down GEMM [2][M][K], gate/up tail [2][2][M][F_tail]
+      c.take<float>(std::max(2 * m * k, 4 * m * plan_up(m, k, n).f_tail));
       break;
     default:
       return -1;
@@ -1036,18 +1074,40 @@ extern "C" int kda_swiglu_bf16(const kda_bf16* x, const kda_bf16* w_up, const kd
   if (f == 0) return hipMemsetAsync(y, 0, (size_t)m * k * 2, as_stream(stream)) == hipSuccess
                          ? KDA_OK : set_error(KDA_ERR_HIP, "swiglu_bf16: memset failed");
   hipStream_t st = as_stream(stream);
-  Params up = make_params(m, f, h, f);
+  const bool have_ws = workspace && aligned16(workspace) &&
+                       workspace_bytes_ >= workspace_bytes(KDA_OP_SWIGLU_BF16, 1, m, k, f, 0);
+  // Gate/up GEMM: the columns that would leave the last round over the device
+  // partly idle (2048 x 14336: 896 tiles = 3.5 rounds on 256 CUs) run as a
+  // split-K pair on the whole device, then a streaming pass applies silu(g)*u.
+  const UpSplit us = have_ws ? plan_up(m, k, f) : UpSplit{f, 0};
+  Params up = make_params(m, us.f_main, h, f);
   add_seg(up, x, k, w_gate, f, k, w_up);
   if (int rc = launch<256, 128, 2, true, Epi::kSwiGLU>(up, 1, st, "swiglu_bf16(up/gate)")) return rc;
+  if (us.f_tail > 0) {
+    float* part = reinterpret_cast<float*>(workspace);
+    Params t = make_params(m, us.f_tail, part, us.f_tail);
+    add_seg(t, x, k, w_gate + us.f_main, f, k / 2, w_up + us.f_main);
+    t.batch_a = k / 2;                     // second half: columns K/2.. of x
+    t.batch_b = (k / 2) * f;               //              rows K/2.. of w_gate, w_up
+    t.batch_c = 2 * m * us.f_tail;         //              its (gate, up) partial pair
+    t.c2_off = m * us.f_tail;              // up partial after the gate partial
+    if (int rc = launch<256, 128, 2, true, Epi::kStoreF32Pair>(t, 2, st, "swiglu_bf16(up/gate tail)"))
+      return rc;
+    const int64_t n4 = m * us.f_tail / 4;
+    const int64_t blocks = std::min<int64_t>((n4 + 255) / 256, (int64_t)device_cu_count() * 16);
+    hipLaunchKernelGGL(swiglu_tail_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                       reinterpret_cast<const floatx4*>(part), reinterpret_cast<uint16_t*>(h) + us.f_main,
+                       m, us.f_tail, f);
+    if (int rc = check_launch("swiglu_bf16(tail silu)")) return rc;
+  }
   // Down GEMM y[M,K] = h[M,F] @ w_down[F,K].  When its 256x256 tiles fill at most
   // half the device (M = 2048, K = 4096: 128 tiles), F is split in two halves that
   // run as a batch of two into fp32 partials, summed into bf16 by a streaming
   // pass: 256 workgroups of the efficient 256x256 tile instead of 256x128 tiles
   // (measured 174 + 15 us against 241 us at 2048x14336x4096).
   const int64_t tiles256 = ((m + 255) / 256) * ((k + 255) / 256);
-  const bool split = 2 * tiles256 <= device_cu_count() && f % (2 * kBK) == 0 && (m * k) % 4 == 0 &&
-                     workspace && aligned16(workspace) &&
-                     workspace_bytes_ >= workspace_bytes(KDA_OP_SWIGLU_BF16, 1, m, k, f, 0);
+  const bool split = have_ws && 2 * tiles256 <= device_cu_count() && f % (2 * kBK) == 0 &&
+                     (m * k) % 4 == 0;
   if (split) {
     float* part = reinterpret_cast<float*>(workspace);
     Params d = make_params(m, k, part, k);
