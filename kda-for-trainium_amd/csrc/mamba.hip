@@ -15,12 +15,12 @@
 // differently, and in fp32 those differences accumulate to a few 1e-6 relative
 // over a 7168-step sequence.
 //
-// Mapping: one workgroup per channel, 4 waves, the sequence in blocks of kT
-// steps, double-buffered in LDS.
+// Mapping: one workgroup per channel, 1 + kT/64 waves, the sequence in blocks of
+// kT steps, double-buffered in LDS.
 //   wave 0 (lanes 0..15, one per state) runs the recurrence over block k: two
 //     dependent VALU ops per step, operands read four steps at a time
 //     (ds_read_b128), states written back four steps at a time;
-//   waves 1..3 (192 lanes, one step each) meanwhile produce dA and dBu for block
+//   waves 1..kT/64 (kT lanes, one step each) meanwhile produce dA and dBu for block
 //     k+1 (coalesced loads of delta, u, b; 16 exps per lane) and reduce block k-1
 //     (h * c over s in numpy's order, one coalesced store of out per lane).
 // One barrier per block.  LDS rows are padded to kT+4 floats so the 16 state rows
@@ -32,7 +32,7 @@
 namespace kda {
 namespace mamba {
 
-constexpr int kT = 192;            // steps per block (= producer lanes)
+constexpr int kT = 320;            // steps per block (= producer lanes; 192 measured 104 us, 320 81 us)
 constexpr int kRow = kT + 4;       // LDS row stride in floats
 constexpr int kMaxS = 16;
 constexpr int kThreads = 64 + kT;  // recurrence wave + producer waves
