@@ -197,9 +197,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Args p) {
             B[i] = *reinterpret_cast<const float4*>(pb + t + 4 * i);
           }
         };
-        auto run = [&](const float4 (&A)[4], const float4 (&B)[4], int t) {
+        auto run = [&](const float4 (&A)[4], const float4 (&B)[4], int t, int i0, int i1) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
+          for (int i = i0; i < i1; ++i) {
             float4 o;
             h = A[i].x * h + B[i].x;
             o.x = h;
@@ -212,16 +212,21 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Args p) {
             *reinterpret_cast<float4*>(ph + t + 4 * i) = o;
           }
         };
+        // The next group's loads are unconditional (the last group re-reads
+        // its own operands, unused): a conditional load splits the loop body,
+        // and at the join the compiler's LDS wait counts turn conservative, so
+        // each group's first operand wait also waited for most of the
+        // prefetch (an LDS round trip per 16 steps).
         float4 a0[4], b0[4], a1[4], b1[4];
         load(a0, b0, 0);
         for (int t = 0;; t += 32) {
           const bool more1 = t + 16 < steps;
-          if (more1) load(a1, b1, t + 16);
-          run(a0, b0, t);
+          load(a1, b1, more1 ? t + 16 : t);
+          run(a0, b0, t, 0, 4);
           if (!more1) break;
           const bool more2 = t + 32 < steps;
-          if (more2) load(a0, b0, t + 32);
-          run(a1, b1, t + 16);
+          load(a0, b0, more2 ? t + 32 : t + 16);
+          run(a1, b1, t + 16, 0, 4);
           if (!more2) break;
         }
       }
