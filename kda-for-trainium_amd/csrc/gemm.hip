@@ -433,12 +433,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(Params p) {
       }
     }
     if constexpr (EPI == Epi::kAddZSsqF32) {
-      // the 4 lanes l, l+16, l+32, l+48 hold the wave's 64 columns of this row
+      // the 4 lanes l, l+16, l+32, l+48 hold the wave's WN columns of this row
       ssq += __shfl_xor(ssq, 16);
       ssq += __shfl_xor(ssq, 32);
-      const int chunk = (n0 + wn * WN) / 64;
+      const int chunk = (n0 + wn * WN) / WN;
       if (row_ok && lane < 16 && n0 + wn * WN < N)
-        p.part[(int64_t)gm * ((N + 63) / 64) + chunk] = ssq;
+        p.part[(int64_t)gm * ((N + WN - 1) / WN) + chunk] = ssq;
     }
   }
 }
@@ -647,10 +647,9 @@ __global__ __launch_bounds__(kRowThreads) void rms_split_f32_kernel(
 //   out[m, n] = y[m, n] * g[n] / sqrt(sum_n y^2 / N + eps)
 __global__ __launch_bounds__(kRowThreads) void row_rmsnorm_f32_kernel(
     float* __restrict__ out, const float* __restrict__ part, const float* __restrict__ g, int n,
-    float eps) {
+    int nchunk, float eps) {
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
-  const int nchunk = (n + 63) / 64;
   float s = 0.f;
   for (int c = tid; c < nchunk; c += kRowThreads) s += part[(int64_t)row * nchunk + c];
 #pragma unroll
@@ -987,7 +986,7 @@ int64_t workspace_bytes(int op, int64_t b, int64_t m, int64_t k, int64_t n, int6
       break;
     case KDA_OP_MATMUL_ADD_RMSNORM_F32:
       plan_split(c, m * k, k * n);
-      c.take<float>(m * ((n + 63) / 64));
+      c.take<float>(m * ((n + 31) / 32));
       break;
     case KDA_OP_BMM_F32:
       plan_split(c, b * m * k, b * k * n);
@@ -1322,17 +1321,25 @@ extern "C" int kda_matmul_add_rmsnorm_f32(const float* x, const float* w, float 
   hipStream_t st = as_stream(stream);
   Carve cv{reinterpret_cast<uint8_t*>(workspace)};
   const SplitPlan s = plan_split(cv, m * k, k * n);
-  float* part = cv.take<float>(m * ((n + 63) / 64));
+  float* part = cv.take<float>(m * ((n + 31) / 32));
   if (int rc = split(x, m * k, s.ah, s.al, st, what)) return rc;
   if (int rc = split(w, k * n, s.bh, s.bl, st, what)) return rc;
   Params p = make_params(m, n, out, n);
   add_split_segs(p, s.ah, s.al, k, s.bh, s.bl, n, k);
   p.z = z;
   p.part = part;
-  // the per-64-column row partials need 64-column wave tiles: 256-wide N tiles
-  if (int rc = launch<256, 256, 1, true, Epi::kAddZSsqF32>(p, 1, st, what)) return rc;
+  // Row partials of the sum of squares: one per wave tile width (64 columns for
+  // 256-wide N tiles, 32 for 128-wide ones, used when 256-wide tiles would leave
+  // CUs idle: 4096x2048 is 128 tiles of 256x256 on 256 CUs).
+  const int64_t tiles256 = ((m + 255) / 256) * ((n + 255) / 256);
+  const bool narrow = tiles256 < device_cu_count();
+  const int64_t nchunk = narrow ? (n + 31) / 32 : (n + 63) / 64;
+  if (int rc = narrow ? (segments_fit(p, 64) ? launch<256, 128, 1, true, Epi::kAddZSsqF32, 64, 2>(p, 1, st, what)
+                                             : launch<256, 128, 1, true, Epi::kAddZSsqF32>(p, 1, st, what))
+                      : launch<256, 256, 1, true, Epi::kAddZSsqF32>(p, 1, st, what))
+    return rc;
   hipLaunchKernelGGL(row_rmsnorm_f32_kernel, dim3((unsigned)m), dim3(kRowThreads), 0, st, out,
-                     part, g, (int)n, eps);
+                     part, g, (int)n, (int)nchunk, eps);
   return check_launch(what);
 }
 
