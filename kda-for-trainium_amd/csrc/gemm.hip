@@ -575,6 +575,13 @@ __global__ __launch_bounds__(256) void splitk2_bf16_kernel(const floatx4* __rest
   }
 }
 
+// Sum of the two fp32 split-K partials [2][n] into fp32 (n % 4 == 0).
+__global__ __launch_bounds__(256) void splitk2_f32_kernel(const floatx4* __restrict__ part,
+                                                          floatx4* __restrict__ y, int64_t n4) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256)
+    y[i] = __builtin_nontemporal_load(part + i) + __builtin_nontemporal_load(part + n4 + i);
+}
+
 // SwiGLU columns computed as split-K partials part[s][q][M][F_tail] (s = k half,
 // q = 0 gate, 1 up): h[m][j] = bf16(silu(g) * u) with g, u the sums of the halves.
 __global__ __launch_bounds__(256) void swiglu_tail_kernel(const floatx4* __restrict__ part,
@@ -931,6 +938,7 @@ struct SwigluPlan {
   uint16_t *xh, *xl, *gh, *gl, *uh, *ul;
   float* h;
   uint16_t *hh, *hl, *dh, *dl;
+  float* part;
 };
 SwigluPlan plan_swiglu(Carve& c, int64_t m, int64_t k, int64_t f) {
   SwigluPlan p;
@@ -945,6 +953,7 @@ SwigluPlan plan_swiglu(Carve& c, int64_t m, int64_t k, int64_t f) {
   p.hl = c.take<uint16_t>(m * f);
   p.dh = c.take<uint16_t>(f * k);
   p.dl = c.take<uint16_t>(f * k);
+  p.part = c.take<float>(2 * m * k);   // split-K partials of the down GEMM
   return p;
 }
 struct RmsBf16Plan {
@@ -1369,6 +1378,24 @@ extern "C" int kda_swiglu_f32(const float* x, const float* w_up, const float* w_
   if (int rc = launch<256, 128, 2, true, Epi::kSwiGLUF32>(up, 1, st, "swiglu_f32(up/gate)")) return rc;
   if (int rc = split(sp.h, m * f, sp.hh, sp.hl, st, what)) return rc;
   if (int rc = split(w_down, f * k, sp.dh, sp.dl, st, what)) return rc;
+  // Down GEMM [M,F]@[F,K]: with fewer 256x128 tiles than half the device
+  // (4096x1024: 128 tiles), F splits in two halves of every product segment,
+  // run as a batch of two into fp32 partials and summed.
+  const int64_t tiles128 = ((m + 255) / 256) * ((k + 127) / 128);
+  if (2 * tiles128 <= device_cu_count() && f % 128 == 0 && (m * k) % 4 == 0) {
+    Params d = make_params(m, k, sp.part, k);
+    add_split_segs(d, sp.hh, sp.hl, f, sp.dh, sp.dl, k, f / 2);
+    d.batch_a = f / 2;         // second half: columns F/2.. of the h planes
+    d.batch_b = (f / 2) * k;   //              rows F/2.. of the w_down planes
+    d.batch_c = m * k;
+    if (int rc = launch<256, 128, 1, true, Epi::kStoreF32, 64, 2>(d, 2, st, "swiglu_f32(down, split-K)"))
+      return rc;
+    const int64_t n4 = m * k / 4;
+    const int64_t blocks = std::min<int64_t>((n4 + 255) / 256, (int64_t)device_cu_count() * 16);
+    hipLaunchKernelGGL(splitk2_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                       reinterpret_cast<const floatx4*>(sp.part), reinterpret_cast<floatx4*>(out), n4);
+    return check_launch("swiglu_f32(split-K sum)");
+  }
   Params down = make_params(m, k, out, k);
   add_split_segs(down, sp.hh, sp.hl, f, sp.dh, sp.dl, k, f);
   return launch_auto<true, Epi::kStoreF32>(down, 1, st, "swiglu_f32(down)");
