@@ -26,8 +26,10 @@
 // One barrier per block.  LDS rows are padded to kT+4 floats so the 16 state rows
 // read by wave 0 fall on distinct banks.
 #include <math.h>
+#include <stddef.h>
 
 #include "common.h"
+#include "lds_dma.h"
 
 namespace kda {
 namespace mamba {
@@ -173,6 +175,116 @@ __device__ __forceinline__ void reduce(const Smem& sm, const Args& p, const floa
   p.out[row + m0 + t] = np_pairwise_sum16(v, p.S);
 }
 
+// The recurrence over `groups` groups of 16 steps of one block, for the state of
+// this lane: h = dA * h + dBu per step (separate multiply and add), h written to
+// LDS after each step.  `da` is the LDS byte address of the lane's dA row (its
+// dBu row follows kDbuOff bytes later), `hs` that of its h row.
+//
+// Inline asm with fixed registers and explicit LDS waits.  Compiled code was
+// measured 13 % slower here: the compiler waited for the whole LDS queue once
+// per 16 steps (its wait counts turn conservative across the loop), and it
+// reused the registers of pending stores for the chain.  In this loop:
+//   operands of group g (v128..v159 or v160..v191, alternately) are read one
+//   group ahead with ds_read_b128, four steps per read;
+//   the chain alternates its four-step outputs between v192..v195 and
+//   v196..v199, so the ds_write_b128 of a quad is two quads old before its
+//   registers are rewritten;
+//   each group starts with lgkmcnt(4): everything but the previous group's four
+//   h stores (issued after the operand reads) has completed, i.e. this group's
+//   operands are in registers.
+// The last group also reads the 16 steps after the block (unused): at most
+// 16 floats past the end of a row, which stays inside Smem (rows are followed
+// by the next row, the dBu array or the h array).
+// The h stores (ds_write_b128) are what is left above the 2-op chain latency:
+// about 7.5 of the 21.5 cycles per step measured on the gfx950 (13.8 without
+// them), independent of where in the chain they are issued.
+#define KDA_S(x) #x
+#define KDA_RD(lo, hi, off) "ds_read_b128 v[" KDA_S(lo) ":" KDA_S(hi) "], %[da] offset:" KDA_S(off) "\n\t"
+#define KDA_WR(lo, hi, off) "ds_write_b128 %[hs], v[" KDA_S(lo) ":" KDA_S(hi) "] offset:" KDA_S(off) "\n\t"
+#define KDA_STEP(o, a, b, hin) \
+  "v_mul_f32 v" KDA_S(o) ", v" KDA_S(a) ", v" KDA_S(hin) "\n\t" \
+  "v_add_f32 v" KDA_S(o) ", v" KDA_S(b) ", v" KDA_S(o) "\n\t"
+// four steps on dA in a0..a3, dBu in b0..b3, h entering in hin; outputs o0..o3,
+// then stored at byte `off` of the group's h row segment
+#define KDA_QUAD(o0, o1, o2, o3, a0, a1, a2, a3, b0, b1, b2, b3, hin, off)                   \
+  KDA_STEP(o0, a0, b0, hin) KDA_STEP(o1, a1, b1, o0) KDA_STEP(o2, a2, b2, o1)                \
+  KDA_STEP(o3, a3, b3, o2) KDA_WR(o0, o3, off)
+// 16 steps on operand set X (dA v128..v143, dBu v144..v159) or Y (v160.., v176..);
+// h enters and leaves in v199
+#define KDA_GROUP_X                                                            \
+  KDA_QUAD(192, 193, 194, 195, 128, 129, 130, 131, 144, 145, 146, 147, 199, 0) \
+  KDA_QUAD(196, 197, 198, 199, 132, 133, 134, 135, 148, 149, 150, 151, 195, 16) \
+  KDA_QUAD(192, 193, 194, 195, 136, 137, 138, 139, 152, 153, 154, 155, 199, 32) \
+  KDA_QUAD(196, 197, 198, 199, 140, 141, 142, 143, 156, 157, 158, 159, 195, 48)
+#define KDA_GROUP_Y                                                            \
+  KDA_QUAD(192, 193, 194, 195, 160, 161, 162, 163, 176, 177, 178, 179, 199, 0) \
+  KDA_QUAD(196, 197, 198, 199, 164, 165, 166, 167, 180, 181, 182, 183, 195, 16) \
+  KDA_QUAD(192, 193, 194, 195, 168, 169, 170, 171, 184, 185, 186, 187, 199, 32) \
+  KDA_QUAD(196, 197, 198, 199, 172, 173, 174, 175, 188, 189, 190, 191, 195, 48)
+// a group's operands into set X / Y: dA at the four offsets past %[da], dBu at
+// the four offsets after them (kDbuOff further on)
+#define KDA_READ_X(off0, off1, off2, off3, boff0, boff1, boff2, boff3)          \
+  KDA_RD(128, 131, off0) KDA_RD(132, 135, off1) KDA_RD(136, 139, off2)         \
+  KDA_RD(140, 143, off3) KDA_RD(144, 147, boff0) KDA_RD(148, 151, boff1)        \
+  KDA_RD(152, 155, boff2) KDA_RD(156, 159, boff3)
+#define KDA_READ_Y(off0, off1, off2, off3, boff0, boff1, boff2, boff3)          \
+  KDA_RD(160, 163, off0) KDA_RD(164, 167, off1) KDA_RD(168, 171, off2)         \
+  KDA_RD(172, 175, off3) KDA_RD(176, 179, boff0) KDA_RD(180, 183, boff1)        \
+  KDA_RD(184, 187, boff2) KDA_RD(188, 191, boff3)
+#define KDA_ADVANCE "v_add_u32 %[da], 64, %[da]\n\tv_add_u32 %[hs], 64, %[hs]\n\t"
+
+constexpr int kDbuOff = 41472;  // bytes from a dA row to its dBu row (spelled out in the asm)
+static_assert(sizeof(Smem::da) == kDbuOff && offsetof(Smem, dbu) == kDbuOff &&
+                  offsetof(Smem, h) == 2 * kDbuOff,
+              "recurrence asm assumes Smem = da, dbu, h with 41472-byte arrays");
+
+__device__ __forceinline__ void recurrence(float& h, uint32_t da, uint32_t hs, int groups) {
+  int left;
+  asm volatile(
+      "s_waitcnt lgkmcnt(0)\n\t"
+      KDA_READ_X(0, 16, 32, 48, 41472, 41488, 41504, 41520)
+      "v_mov_b32 v199, %[h]\n\t"
+      "s_mov_b32 %[left], %[groups]\n\t"
+      "s_waitcnt lgkmcnt(0)\n\t"
+      "L_mamba_rec_%=:\n\t"
+      "s_waitcnt lgkmcnt(4)\n\t"
+      KDA_READ_Y(64, 80, 96, 112, 41536, 41552, 41568, 41584)
+      KDA_GROUP_X
+      KDA_ADVANCE
+      "s_sub_u32 %[left], %[left], 1\n\t"
+      "s_cmp_eq_u32 %[left], 0\n\t"
+      "s_cbranch_scc1 L_mamba_rec_end_%=\n\t"
+      "s_waitcnt lgkmcnt(4)\n\t"
+      KDA_READ_X(64, 80, 96, 112, 41536, 41552, 41568, 41584)
+      KDA_GROUP_Y
+      KDA_ADVANCE
+      "s_sub_u32 %[left], %[left], 1\n\t"
+      "s_cmp_eq_u32 %[left], 0\n\t"
+      "s_cbranch_scc0 L_mamba_rec_%=\n\t"
+      "L_mamba_rec_end_%=:\n\t"
+      "s_waitcnt lgkmcnt(0)\n\t"
+      "v_mov_b32 %[h], v199"
+      : [h] "+v"(h), [da] "+v"(da), [hs] "+v"(hs), [left] "=&s"(left)
+      : [groups] "s"(groups)
+      : "memory", "scc", "v128", "v129", "v130", "v131", "v132", "v133", "v134", "v135", "v136",
+        "v137", "v138", "v139", "v140", "v141", "v142", "v143", "v144", "v145", "v146", "v147",
+        "v148", "v149", "v150", "v151", "v152", "v153", "v154", "v155", "v156", "v157", "v158",
+        "v159", "v160", "v161", "v162", "v163", "v164", "v165", "v166", "v167", "v168", "v169",
+        "v170", "v171", "v172", "v173", "v174", "v175", "v176", "v177", "v178", "v179", "v180",
+        "v181", "v182", "v183", "v184", "v185", "v186", "v187", "v188", "v189", "v190", "v191",
+        "v192", "v193", "v194", "v195", "v196", "v197", "v198", "v199");
+}
+#undef KDA_S
+#undef KDA_RD
+#undef KDA_WR
+#undef KDA_STEP
+#undef KDA_QUAD
+#undef KDA_GROUP_X
+#undef KDA_GROUP_Y
+#undef KDA_READ_X
+#undef KDA_READ_Y
+#undef KDA_ADVANCE
+
 __global__ __launch_bounds__(kThreads) void scan_kernel(Args p) {
   __shared__ __align__(16) Smem sm;
   const int64_t row = (int64_t)blockIdx.x * p.M;
@@ -185,51 +297,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Args p) {
     for (int k = 0; k < p.nb; ++k) {
       const int buf = k & 1;
       const int steps = (min(kT, p.M - k * kT) + 15) & ~15;
-      if (s < kMaxS) {
-        const float* pa = &sm.da[buf][s][0];
-        const float* pb = &sm.dbu[buf][s][0];
-        float* ph = &sm.h[buf][s][0];
-        // 16 steps per group; the next group's operands are read while this one runs
-        auto load = [&](float4 (&A)[4], float4 (&B)[4], int t) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            A[i] = *reinterpret_cast<const float4*>(pa + t + 4 * i);
-            B[i] = *reinterpret_cast<const float4*>(pb + t + 4 * i);
-          }
-        };
-        auto run = [&](const float4 (&A)[4], const float4 (&B)[4], int t, int i0, int i1) {
-#pragma unroll
-          for (int i = i0; i < i1; ++i) {
-            float4 o;
-            h = A[i].x * h + B[i].x;
-            o.x = h;
-            h = A[i].y * h + B[i].y;
-            o.y = h;
-            h = A[i].z * h + B[i].z;
-            o.z = h;
-            h = A[i].w * h + B[i].w;
-            o.w = h;
-            *reinterpret_cast<float4*>(ph + t + 4 * i) = o;
-          }
-        };
-        // The next group's loads are unconditional (the last group re-reads
-        // its own operands, unused): a conditional load splits the loop body,
-        // and at the join the compiler's LDS wait counts turn conservative, so
-        // each group's first operand wait also waited for most of the
-        // prefetch (an LDS round trip per 16 steps).
-        float4 a0[4], b0[4], a1[4], b1[4];
-        load(a0, b0, 0);
-        for (int t = 0;; t += 32) {
-          const bool more1 = t + 16 < steps;
-          load(a1, b1, more1 ? t + 16 : t);
-          run(a0, b0, t, 0, 4);
-          if (!more1) break;
-          const bool more2 = t + 32 < steps;
-          load(a0, b0, more2 ? t + 32 : t + 16);
-          run(a1, b1, t + 16, 0, 4);
-          if (!more2) break;
-        }
-      }
+      if (s < kMaxS) recurrence(h, lds_addr(&sm.da[buf][s][0]), lds_addr(&sm.h[buf][s][0]), steps / 16);
       __syncthreads();  // block k consumed and its states written
     }
   } else {
