@@ -16,13 +16,16 @@
 // over a 7168-step sequence.
 //
 // Mapping: one workgroup per channel, 1 + kT/64 waves, the sequence in blocks of
-// kT steps, double-buffered in LDS.
+// kT steps; dA/dBu triple-buffered in LDS, state checkpoints double-buffered.
 //   wave 0 (lanes 0..15, one per state) runs the recurrence over block k: two
 //     dependent VALU ops per step, operands read four steps at a time
-//     (ds_read_b128), states written back four steps at a time;
+//     (ds_read_b128); it stores h only after every second step (a checkpoint),
+//     two ds_write_b128 per 16 steps;
 //   waves 1..kT/64 (kT lanes, one step each) meanwhile produce dA and dBu for block
-//     k+1 (coalesced loads of delta, u, b; 16 exps per lane) and reduce block k-1
-//     (h * c over s in numpy's order, one coalesced store of out per lane).
+//     k+1 (coalesced loads of delta, u, b; 16 exps per lane) and reduce block k-1:
+//     each lane recomputes h of its step from the checkpoint before its step pair
+//     with the same multiply and add (bit-identical), then sums h * c over s in
+//     numpy's order and stores out (coalesced).
 // One barrier per block.  LDS rows are padded to kT+4 floats so the 16 state rows
 // read by wave 0 fall on distinct banks.
 #include <math.h>
@@ -34,8 +37,9 @@
 namespace kda {
 namespace mamba {
 
-constexpr int kT = 320;            // steps per block (= producer lanes; 192 measured 104 us, 320 81 us)
+constexpr int kT = 320;            // steps per block (= producer lanes; 192 measured 23 % slower)
 constexpr int kRow = kT + 4;       // LDS row stride in floats
+constexpr int kCkRow = 4 + kT / 2; // checkpoint row: [3] = h entering the block, [4 + i] = h after pair i
 constexpr int kMaxS = 16;
 constexpr int kThreads = 64 + kT;  // recurrence wave + producer waves
 
@@ -65,27 +69,54 @@ struct Args {
 // general division (v_div_scale / v_div_fmas / v_div_fixup around a reciprocal
 // and three Newton/remainder steps) neither scales nor fixes up, so the core
 // sequence alone below gives the same correctly rounded quotient.
-__device__ __forceinline__ float np_expf(float x) {
+//
+// Evaluates N arguments in place, each step applied to all N before the next
+// (N = 1 in the scan: interleaving eight exps by hand was measured 6 % slower
+// there than the compiler's own schedule).
+template <int N>
+__device__ __forceinline__ void np_expf_n(float (&x)[N]) {
   const float kXmax = 0x1.62e43p+6f;    //  88.72283935546875
   const float kXmin = -0x1.9fe36ap+6f;  // -103.97208404541015625
-  const float k = __builtin_rintf(x * 0x1.715476p+0f);  // log2(e); ties to even
-  float r = __builtin_fmaf(k, -0x1.62e4p-1f, x);
-  r = __builtin_fmaf(k, -0x1.7f7d1cp-20f, r);
-  float n = __builtin_fmaf(0x1.0a7bbp-11f, r, 0x1.bae2b2p-8f);
-  n = __builtin_fmaf(n, r, 0x1.a2fb18p-5f);
-  n = __builtin_fmaf(n, r, 0x1.fa98bp-3f);
-  n = __builtin_fmaf(n, r, 0x1.7397aap-1f);
-  n = __builtin_fmaf(n, r, 1.0f);
-  float d = __builtin_fmaf(0x1.61d064p-6f, r, -0x1.18d0aep-2f);
-  d = __builtin_fmaf(d, r, 1.0f);
-  float y = __builtin_amdgcn_rcpf(d);
-  y = __builtin_fmaf(__builtin_fmaf(-d, y, 1.0f), y, y);
-  float q = n * y;
-  q = __builtin_fmaf(__builtin_fmaf(-d, q, n), y, q);
-  q = __builtin_fmaf(__builtin_fmaf(-d, q, n), y, q);
-  float e = __builtin_ldexpf(q, (int)k);
-  e = (x >= kXmax) ? __builtin_inff() : e;
-  return (x <= kXmin) ? 0.f : e;
+  float k[N], r[N], n[N], d[N], y[N], q[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) k[j] = __builtin_rintf(x[j] * 0x1.715476p+0f);  // log2(e); ties to even
+#pragma unroll
+  for (int j = 0; j < N; ++j) r[j] = __builtin_fmaf(k[j], -0x1.62e4p-1f, x[j]);
+#pragma unroll
+  for (int j = 0; j < N; ++j) r[j] = __builtin_fmaf(k[j], -0x1.7f7d1cp-20f, r[j]);
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    n[j] = __builtin_fmaf(0x1.0a7bbp-11f, r[j], 0x1.bae2b2p-8f);
+    d[j] = __builtin_fmaf(0x1.61d064p-6f, r[j], -0x1.18d0aep-2f);
+  }
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    n[j] = __builtin_fmaf(n[j], r[j], 0x1.a2fb18p-5f);
+    d[j] = __builtin_fmaf(d[j], r[j], 1.0f);
+  }
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    n[j] = __builtin_fmaf(n[j], r[j], 0x1.fa98bp-3f);
+    y[j] = __builtin_amdgcn_rcpf(d[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < N; ++j) n[j] = __builtin_fmaf(n[j], r[j], 0x1.7397aap-1f);
+#pragma unroll
+  for (int j = 0; j < N; ++j) y[j] = __builtin_fmaf(__builtin_fmaf(-d[j], y[j], 1.0f), y[j], y[j]);
+#pragma unroll
+  for (int j = 0; j < N; ++j) n[j] = __builtin_fmaf(n[j], r[j], 1.0f);
+#pragma unroll
+  for (int j = 0; j < N; ++j) q[j] = n[j] * y[j];
+#pragma unroll
+  for (int j = 0; j < N; ++j) q[j] = __builtin_fmaf(__builtin_fmaf(-d[j], q[j], n[j]), y[j], q[j]);
+#pragma unroll
+  for (int j = 0; j < N; ++j) q[j] = __builtin_fmaf(__builtin_fmaf(-d[j], q[j], n[j]), y[j], q[j]);
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    float e = __builtin_ldexpf(q[j], (int)k[j]);
+    e = (x[j] >= kXmax) ? __builtin_inff() : e;
+    x[j] = (x[j] <= kXmin) ? 0.f : e;
+  }
 }
 
 // numpy's pairwise summation of n <= 16 contiguous floats (the reduction loop of
@@ -112,10 +143,13 @@ __device__ __forceinline__ float np_pairwise_sum16(const float (&v)[kMaxS], int 
   return o;
 }
 
+// dA/dBu of block k live in buffer k % 3 (produced in iteration k-1, consumed by
+// the recurrence in iteration k, re-read by the reduction in iteration k+1); the
+// checkpoints of block k in buffer k % 2 (written in iteration k, read in k+1).
 struct Smem {
-  float da[2][kMaxS][kRow];
-  float dbu[2][kMaxS][kRow];
-  float h[2][kMaxS][kRow];
+  float da[3][kMaxS][kRow];
+  float dbu[3][kMaxS][kRow];
+  float ck[2][kMaxS][kCkRow];
 };
 
 // Per-step inputs of one block, held in registers one block ahead of their use.
@@ -143,17 +177,19 @@ __device__ __forceinline__ void load_c(float (&cv)[kMaxS], const Args& p, int t,
 
 // dA and dBu of step t of block `blk` into buffer `buf`; the padding steps up to
 // the next multiple of 16 get dA = 1, dBu = 0 (the recurrence passes h through
-// them unchanged); states s >= S get 0 (h stays 0).
+// them unchanged).  States s >= S are computed from a = b = 0 like the others:
+// a per-state condition here became 16 branches (2 % slower); their h never
+// reaches the output (the reduction masks s >= S).
 __device__ __forceinline__ void produce(Smem& sm, const Args& p, const StepIn& x,
                                         const float (&av)[kMaxS], int t, int blk, int buf) {
   const int len = min(kT, p.M - blk * kT);
   if (t < len) {
 #pragma unroll
     for (int s = 0; s < kMaxS; ++s) {
-      const float da = np_expf(x.d * av[s]);
-      const float dbu = (x.d * x.b[s]) * x.u;
-      sm.da[buf][s][t] = (s < p.S) ? da : 0.f;
-      sm.dbu[buf][s][t] = (s < p.S) ? dbu : 0.f;
+      float e[1] = {x.d * av[s]};
+      np_expf_n(e);
+      sm.da[buf][s][t] = e[0];
+      sm.dbu[buf][s][t] = (x.d * x.b[s]) * x.u;
     }
   } else if (t < ((len + 15) & ~15)) {
 #pragma unroll
@@ -164,63 +200,93 @@ __device__ __forceinline__ void produce(Smem& sm, const Args& p, const StepIn& x
   }
 }
 
-// out[m0 + t] = sum_s h[s][t] * c[s][m0 + t] for the block in buffer `buf`
+// out[m0 + t] = sum_s h[s][t] * c[s][m0 + t] for block `blk` (dA/dBu in buffer
+// `buf`, checkpoints in `cbuf`).  h[s][t] is recomputed from the checkpoint h
+// before the step pair of t over the pair's steps up to t, with the
+// recurrence's own multiply and add, so it equals the value the recurrence had.
 __device__ __forceinline__ void reduce(const Smem& sm, const Args& p, const float (&cv)[kMaxS],
-                                       int64_t row, int t, int blk, int buf) {
+                                       int64_t row, int t, int blk, int buf, int cbuf) {
   const int m0 = blk * kT;
   if (t >= min(kT, p.M - m0)) return;
+  const int q = t & 1, t0 = t - q;
   float v[kMaxS];
+  // Eight states at a time: all LDS reads first, then both steps of the pair
+  // computed unconditionally (the empty asm keeps the compiler from turning the
+  // per-lane choice of step into branches, which serialised the reads state by
+  // state) and the step of this lane selected.
 #pragma unroll
-  for (int s = 0; s < kMaxS; ++s) v[s] = (s < p.S) ? sm.h[buf][s][t] * cv[s] : 0.f;
+  for (int s0 = 0; s0 < kMaxS; s0 += 8) {
+    float2 a[8], b[8];
+    float h0[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      a[j] = *reinterpret_cast<const float2*>(&sm.da[buf][s0 + j][t0]);
+      b[j] = *reinterpret_cast<const float2*>(&sm.dbu[buf][s0 + j][t0]);
+      h0[j] = sm.ck[cbuf][s0 + j][3 + t0 / 2];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float h1 = a[j].x * h0[j] + b[j].x;
+      const float h2 = a[j].y * h1 + b[j].y;
+      asm volatile("" ::"v"(h1), "v"(h2));
+      const float h = q ? h2 : h1;
+      v[s0 + j] = (s0 + j < p.S) ? h * cv[s0 + j] : 0.f;
+    }
+  }
   p.out[row + m0 + t] = np_pairwise_sum16(v, p.S);
 }
 
 // The recurrence over `groups` groups of 16 steps of one block, for the state of
-// this lane: h = dA * h + dBu per step (separate multiply and add), h written to
-// LDS after each step.  `da` is the LDS byte address of the lane's dA row (its
-// dBu row follows kDbuOff bytes later), `hs` that of its h row.
+// this lane: h = dA * h + dBu per step (separate multiply and add).  `da` is the
+// LDS byte address of the lane's dA row (its dBu row follows kDbuOff bytes
+// later), `ck` that of its checkpoint row: h entering the block goes to entry 3,
+// h after step pair i of the block to entry 4 + i.
 //
 // Inline asm with fixed registers and explicit LDS waits.  Compiled code was
-// measured 13 % slower here: the compiler waited for the whole LDS queue once
-// per 16 steps (its wait counts turn conservative across the loop), and it
-// reused the registers of pending stores for the chain.  In this loop:
-//   operands of group g (v128..v159 or v160..v191, alternately) are read one
-//   group ahead with ds_read_b128, four steps per read;
-//   the chain alternates its four-step outputs between v192..v195 and
-//   v196..v199, so the ds_write_b128 of a quad is two quads old before its
-//   registers are rewritten;
-//   each group starts with lgkmcnt(4): everything but the previous group's four
-//   h stores (issued after the operand reads) has completed, i.e. this group's
-//   operands are in registers.
+// measured 13 % slower with per-step h stores: the compiler waited for the whole
+// LDS queue once per 16 steps (its wait counts turn conservative across the
+// loop) and reused the registers of pending stores for the chain.  Stores are
+// what costs here: a ds_write_b128 of h every 4 steps added 7.5 cycles per step
+// to the 13.8 of the bare 2-op chain (gfx950), wherever it was placed.  Storing
+// h after every second step halves that; the reduction recomputes the step in
+// between (checkpoints every 4 steps made the reduction's recomputation the
+// bottleneck instead).  In this loop:
+//   operands of group g (dA, dBu: v128..v159 or v160..v191, alternately) are
+//   read one group ahead with ds_read_b128, four steps per read;
+//   each step pair runs its first step into v192 and its second into a
+//   checkpoint register (v200..v207 for groups on the first operand set,
+//   v208..v215 on the second), which also carries h into the next pair; the
+//   eight checkpoints of a group go out in two ds_write_b128 and are not
+//   rewritten for another group;
+//   each group starts with lgkmcnt(2): all but the previous group's two
+//   checkpoint stores (issued after the operand reads) have completed, i.e. this
+//   group's operands are in registers.
 // The last group also reads the 16 steps after the block (unused): at most
-// 16 floats past the end of a row, which stays inside Smem (rows are followed
-// by the next row, the dBu array or the h array).
-// The h stores (ds_write_b128) are what is left above the 2-op chain latency:
-// about 7.5 of the 21.5 cycles per step measured on the gfx950 (13.8 without
-// them), independent of where in the chain they are issued.
+// 16 floats past the end of a row, which stays inside Smem (a row is followed by
+// the next row, the dBu array or the checkpoint array).
 #define KDA_S(x) #x
 #define KDA_RD(lo, hi, off) "ds_read_b128 v[" KDA_S(lo) ":" KDA_S(hi) "], %[da] offset:" KDA_S(off) "\n\t"
-#define KDA_WR(lo, hi, off) "ds_write_b128 %[hs], v[" KDA_S(lo) ":" KDA_S(hi) "] offset:" KDA_S(off) "\n\t"
 #define KDA_STEP(o, a, b, hin) \
   "v_mul_f32 v" KDA_S(o) ", v" KDA_S(a) ", v" KDA_S(hin) "\n\t" \
   "v_add_f32 v" KDA_S(o) ", v" KDA_S(b) ", v" KDA_S(o) "\n\t"
-// four steps on dA in a0..a3, dBu in b0..b3, h entering in hin; outputs o0..o3,
-// then stored at byte `off` of the group's h row segment
-#define KDA_QUAD(o0, o1, o2, o3, a0, a1, a2, a3, b0, b1, b2, b3, hin, off)                   \
-  KDA_STEP(o0, a0, b0, hin) KDA_STEP(o1, a1, b1, o0) KDA_STEP(o2, a2, b2, o1)                \
-  KDA_STEP(o3, a3, b3, o2) KDA_WR(o0, o3, off)
-// 16 steps on operand set X (dA v128..v143, dBu v144..v159) or Y (v160.., v176..);
-// h enters and leaves in v199
-#define KDA_GROUP_X                                                            \
-  KDA_QUAD(192, 193, 194, 195, 128, 129, 130, 131, 144, 145, 146, 147, 199, 0) \
-  KDA_QUAD(196, 197, 198, 199, 132, 133, 134, 135, 148, 149, 150, 151, 195, 16) \
-  KDA_QUAD(192, 193, 194, 195, 136, 137, 138, 139, 152, 153, 154, 155, 199, 32) \
-  KDA_QUAD(196, 197, 198, 199, 140, 141, 142, 143, 156, 157, 158, 159, 195, 48)
-#define KDA_GROUP_Y                                                            \
-  KDA_QUAD(192, 193, 194, 195, 160, 161, 162, 163, 176, 177, 178, 179, 199, 0) \
-  KDA_QUAD(196, 197, 198, 199, 164, 165, 166, 167, 180, 181, 182, 183, 195, 16) \
-  KDA_QUAD(192, 193, 194, 195, 168, 169, 170, 171, 184, 185, 186, 187, 199, 32) \
-  KDA_QUAD(196, 197, 198, 199, 172, 173, 174, 175, 188, 189, 190, 191, 195, 48)
+// two steps on dA in a0, a1, dBu in b0, b1, h entering in hin, leaving in ck
+#define KDA_PAIR(a0, a1, b0, b1, hin, ck) KDA_STEP(192, a0, b0, hin) KDA_STEP(ck, a1, b1, 192)
+// 16 steps on operand set X (dA v128..v143, dBu v144..v159; checkpoints
+// v200..v207, h entering in v215) or Y (v160.., v176..; v208..v215, h in v207)
+#define KDA_GROUP_X                                                                     \
+  KDA_PAIR(128, 129, 144, 145, 215, 200) KDA_PAIR(130, 131, 146, 147, 200, 201)         \
+  KDA_PAIR(132, 133, 148, 149, 201, 202) KDA_PAIR(134, 135, 150, 151, 202, 203)         \
+  "ds_write_b128 %[ck], v[200:203] offset:16\n\t"                                        \
+  KDA_PAIR(136, 137, 152, 153, 203, 204) KDA_PAIR(138, 139, 154, 155, 204, 205)         \
+  KDA_PAIR(140, 141, 156, 157, 205, 206) KDA_PAIR(142, 143, 158, 159, 206, 207)         \
+  "ds_write_b128 %[ck], v[204:207] offset:32\n\t"
+#define KDA_GROUP_Y                                                                     \
+  KDA_PAIR(160, 161, 176, 177, 207, 208) KDA_PAIR(162, 163, 178, 179, 208, 209)         \
+  KDA_PAIR(164, 165, 180, 181, 209, 210) KDA_PAIR(166, 167, 182, 183, 210, 211)         \
+  "ds_write_b128 %[ck], v[208:211] offset:16\n\t"                                        \
+  KDA_PAIR(168, 169, 184, 185, 211, 212) KDA_PAIR(170, 171, 186, 187, 212, 213)         \
+  KDA_PAIR(172, 173, 188, 189, 213, 214) KDA_PAIR(174, 175, 190, 191, 214, 215)         \
+  "ds_write_b128 %[ck], v[212:215] offset:32\n\t"
 // a group's operands into set X / Y: dA at the four offsets past %[da], dBu at
 // the four offsets after them (kDbuOff further on)
 #define KDA_READ_X(off0, off1, off2, off3, boff0, boff1, boff2, boff3)          \
@@ -231,40 +297,44 @@ __device__ __forceinline__ void reduce(const Smem& sm, const Args& p, const floa
   KDA_RD(160, 163, off0) KDA_RD(164, 167, off1) KDA_RD(168, 171, off2)         \
   KDA_RD(172, 175, off3) KDA_RD(176, 179, boff0) KDA_RD(180, 183, boff1)        \
   KDA_RD(184, 187, boff2) KDA_RD(188, 191, boff3)
-#define KDA_ADVANCE "v_add_u32 %[da], 64, %[da]\n\tv_add_u32 %[hs], 64, %[hs]\n\t"
+#define KDA_ADVANCE "v_add_u32 %[da], 64, %[da]\n\tv_add_u32 %[ck], 32, %[ck]\n\t"
 
-constexpr int kDbuOff = 41472;  // bytes from a dA row to its dBu row (spelled out in the asm)
+constexpr int kDbuOff = 62208;  // bytes from a dA row to its dBu row (spelled out in the asm)
 static_assert(sizeof(Smem::da) == kDbuOff && offsetof(Smem, dbu) == kDbuOff &&
-                  offsetof(Smem, h) == 2 * kDbuOff,
-              "recurrence asm assumes Smem = da, dbu, h with 41472-byte arrays");
+                  offsetof(Smem, ck) == 2 * kDbuOff && kCkRow % 4 == 0,
+              "recurrence asm assumes Smem = da, dbu (62208 bytes each), ck");
 
-__device__ __forceinline__ void recurrence(float& h, uint32_t da, uint32_t hs, int groups) {
+__device__ __forceinline__ void recurrence(float& h, uint32_t da, uint32_t ck, int groups) {
   int left;
   asm volatile(
       "s_waitcnt lgkmcnt(0)\n\t"
-      KDA_READ_X(0, 16, 32, 48, 41472, 41488, 41504, 41520)
-      "v_mov_b32 v199, %[h]\n\t"
+      KDA_READ_X(0, 16, 32, 48, 62208, 62224, 62240, 62256)
+      "v_mov_b32 v215, %[h]\n\t"
+      "ds_write_b32 %[ck], v215 offset:12\n\t"
       "s_mov_b32 %[left], %[groups]\n\t"
       "s_waitcnt lgkmcnt(0)\n\t"
       "L_mamba_rec_%=:\n\t"
-      "s_waitcnt lgkmcnt(4)\n\t"
-      KDA_READ_Y(64, 80, 96, 112, 41536, 41552, 41568, 41584)
+      "s_waitcnt lgkmcnt(2)\n\t"
+      KDA_READ_Y(64, 80, 96, 112, 62272, 62288, 62304, 62320)
       KDA_GROUP_X
       KDA_ADVANCE
       "s_sub_u32 %[left], %[left], 1\n\t"
       "s_cmp_eq_u32 %[left], 0\n\t"
-      "s_cbranch_scc1 L_mamba_rec_end_%=\n\t"
-      "s_waitcnt lgkmcnt(4)\n\t"
-      KDA_READ_X(64, 80, 96, 112, 41536, 41552, 41568, 41584)
+      "s_cbranch_scc1 L_mamba_rec_end_x_%=\n\t"
+      "s_waitcnt lgkmcnt(2)\n\t"
+      KDA_READ_X(64, 80, 96, 112, 62272, 62288, 62304, 62320)
       KDA_GROUP_Y
       KDA_ADVANCE
       "s_sub_u32 %[left], %[left], 1\n\t"
       "s_cmp_eq_u32 %[left], 0\n\t"
       "s_cbranch_scc0 L_mamba_rec_%=\n\t"
-      "L_mamba_rec_end_%=:\n\t"
-      "s_waitcnt lgkmcnt(0)\n\t"
-      "v_mov_b32 %[h], v199"
-      : [h] "+v"(h), [da] "+v"(da), [hs] "+v"(hs), [left] "=&s"(left)
+      "v_mov_b32 %[h], v215\n\t"
+      "s_branch L_mamba_rec_done_%=\n\t"
+      "L_mamba_rec_end_x_%=:\n\t"
+      "v_mov_b32 %[h], v207\n\t"
+      "L_mamba_rec_done_%=:\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : [h] "+v"(h), [da] "+v"(da), [ck] "+v"(ck), [left] "=&s"(left)
       : [groups] "s"(groups)
       : "memory", "scc", "v128", "v129", "v130", "v131", "v132", "v133", "v134", "v135", "v136",
         "v137", "v138", "v139", "v140", "v141", "v142", "v143", "v144", "v145", "v146", "v147",
@@ -272,13 +342,13 @@ __device__ __forceinline__ void recurrence(float& h, uint32_t da, uint32_t hs, i
         "v159", "v160", "v161", "v162", "v163", "v164", "v165", "v166", "v167", "v168", "v169",
         "v170", "v171", "v172", "v173", "v174", "v175", "v176", "v177", "v178", "v179", "v180",
         "v181", "v182", "v183", "v184", "v185", "v186", "v187", "v188", "v189", "v190", "v191",
-        "v192", "v193", "v194", "v195", "v196", "v197", "v198", "v199");
+        "v192", "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209",
+        "v210", "v211", "v212", "v213", "v214", "v215");
 }
 #undef KDA_S
 #undef KDA_RD
-#undef KDA_WR
 #undef KDA_STEP
-#undef KDA_QUAD
+#undef KDA_PAIR
 #undef KDA_GROUP_X
 #undef KDA_GROUP_Y
 #undef KDA_READ_X
@@ -295,10 +365,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Args p) {
     float h = 0.f;
     __syncthreads();  // block 0 produced
     for (int k = 0; k < p.nb; ++k) {
-      const int buf = k & 1;
       const int steps = (min(kT, p.M - k * kT) + 15) & ~15;
-      if (s < kMaxS) recurrence(h, lds_addr(&sm.da[buf][s][0]), lds_addr(&sm.h[buf][s][0]), steps / 16);
-      __syncthreads();  // block k consumed and its states written
+      if (s < kMaxS)
+        recurrence(h, lds_addr(&sm.da[k % 3][s][0]), lds_addr(&sm.ck[k & 1][s][0]), steps / 16);
+      __syncthreads();  // block k consumed and its checkpoints written
     }
   } else {
     const int t = tid - 64;
@@ -319,11 +389,11 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Args p) {
 #pragma unroll
       for (int s = 0; s < kMaxS; ++s) c_use[s] = c_nxt[s];  // block k-1
       load_c(c_nxt, p, t, k);
-      if (k + 1 < p.nb) produce(sm, p, cur, av, t, k + 1, (k + 1) & 1);
-      if (k >= 1) reduce(sm, p, c_use, row, t, k - 1, (k - 1) & 1);
-      __syncthreads();  // block k's states written by the recurrence wave
+      if (k + 1 < p.nb) produce(sm, p, cur, av, t, k + 1, (k + 1) % 3);
+      if (k >= 1) reduce(sm, p, c_use, row, t, k - 1, (k - 1) % 3, (k - 1) & 1);
+      __syncthreads();  // block k's checkpoints written by the recurrence wave
     }
-    reduce(sm, p, c_nxt, row, t, p.nb - 1, (p.nb - 1) & 1);
+    reduce(sm, p, c_nxt, row, t, p.nb - 1, (p.nb - 1) % 3, (p.nb - 1) & 1);
   }
 }
 
