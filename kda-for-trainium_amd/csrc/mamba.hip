@@ -162,8 +162,10 @@ __device__ __forceinline__ void load_step(StepIn& x, const Args& p, int64_t row,
   if (blk < p.nb && t < p.M - m0) {
     x.d = p.delta[row + m0 + t];
     x.u = p.u[row + m0 + t];
+    // rows s >= S repeat row S-1 (no per-state condition, which became 16
+    // branches): those states never reach the output
 #pragma unroll
-    for (int s = 0; s < kMaxS; ++s) x.b[s] = (s < p.S) ? p.b[(int64_t)s * p.M + m0 + t] : 0.f;
+    for (int s = 0; s < kMaxS; ++s) x.b[s] = p.b[(int64_t)min(s, p.S - 1) * p.M + m0 + t];
   }
 }
 
@@ -171,15 +173,15 @@ __device__ __forceinline__ void load_c(float (&cv)[kMaxS], const Args& p, int t,
   const int m0 = blk * kT;
   if (t < p.M - m0) {
 #pragma unroll
-    for (int s = 0; s < kMaxS; ++s) cv[s] = (s < p.S) ? p.c[(int64_t)s * p.M + m0 + t] : 0.f;
+    for (int s = 0; s < kMaxS; ++s) cv[s] = p.c[(int64_t)min(s, p.S - 1) * p.M + m0 + t];
   }
 }
 
 // dA and dBu of step t of block `blk` into buffer `buf`; the padding steps up to
 // the next multiple of 16 get dA = 1, dBu = 0 (the recurrence passes h through
-// them unchanged).  States s >= S are computed from a = b = 0 like the others:
-// a per-state condition here became 16 branches (2 % slower); their h never
-// reaches the output (the reduction masks s >= S).
+// them unchanged).  States s >= S are computed like the others (from a = 0 and
+// row S-1 of b): a per-state condition here became 16 branches (2 % slower);
+// their h never reaches the output (the reduction masks s >= S).
 __device__ __forceinline__ void produce(Smem& sm, const Args& p, const StepIn& x,
                                         const float (&av)[kMaxS], int t, int blk, int buf) {
   const int len = min(kT, p.M - blk * kT);
