@@ -10,7 +10,12 @@
 namespace kda {
 namespace {
 
+// Threads per workgroup.  Measured on MI355X: SiLU (2 streams) runs best with
+// 256 (128: 2 % slower); AdamW (7 streams) and RoPE (5 streams) with 128
+// (256: 8 % and 6 % slower, 64 no better).
 constexpr int kBlock = 256;
+constexpr int kAdamBlock = 128;
+constexpr int kRopeBlock = 128;
 // 16-byte vectors per thread (per stream).  Measured on MI355X (SiLU over
 // 2 x 64 MiB, a 7-stream AdamW update over 7 x 512 MiB): one vector per thread
 // beats 2 and 4 -- more workgroups in flight per CU hide more latency than
@@ -74,18 +79,18 @@ __device__ __forceinline__ void adam1(float& p, float g, float& m, float& v, con
 }
 
 template <bool kWriteMoments>
-__global__ __launch_bounds__(kBlock) void adamw_vec_kernel(const floatx4* p_in, const floatx4* g_in,
+__global__ __launch_bounds__(kAdamBlock) void adamw_vec_kernel(const floatx4* p_in, const floatx4* g_in,
                                                            const floatx4* m_in, const floatx4* v_in,
                                                            floatx4* p_out, floatx4* m_out,
                                                            floatx4* v_out, int64_t n4,
                                                            AdamParams a) {
   // p_out may alias p_in (and m_out/v_out alias m_in/v_in): every element is
   // loaded by the thread that later stores it, and all loads precede all stores.
-  const int64_t base = (int64_t)blockIdx.x * (kBlock * kAdamUnroll) + threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * (kAdamBlock * kAdamUnroll) + threadIdx.x;
   floatx4 p[kAdamUnroll], g[kAdamUnroll], m[kAdamUnroll], v[kAdamUnroll];
 #pragma unroll
   for (int u = 0; u < kAdamUnroll; ++u) {
-    const int64_t i = base + (int64_t)u * kBlock;
+    const int64_t i = base + (int64_t)u * kAdamBlock;
     if (i < n4) {
       p[u] = __builtin_nontemporal_load(p_in + i);
       g[u] = __builtin_nontemporal_load(g_in + i);
@@ -95,7 +100,7 @@ __global__ __launch_bounds__(kBlock) void adamw_vec_kernel(const floatx4* p_in, 
   }
 #pragma unroll
   for (int u = 0; u < kAdamUnroll; ++u) {
-    const int64_t i = base + (int64_t)u * kBlock;
+    const int64_t i = base + (int64_t)u * kAdamBlock;
     if (i < n4) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -114,12 +119,12 @@ __global__ __launch_bounds__(kBlock) void adamw_vec_kernel(const floatx4* p_in, 
   }
 }
 
-__global__ __launch_bounds__(kBlock) void adamw_scalar_kernel(const float* p_in, const float* g_in,
+__global__ __launch_bounds__(kAdamBlock) void adamw_scalar_kernel(const float* p_in, const float* g_in,
                                                               const float* m_in, const float* v_in,
                                                               float* p_out, float* m_out,
                                                               float* v_out, int64_t begin,
                                                               int64_t n, AdamParams a) {
-  const int64_t i = begin + (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t i = begin + (int64_t)blockIdx.x * kAdamBlock + threadIdx.x;
   if (i >= n) return;
   float p = p_in[i], m = m_in[i], v = v_in[i];
   adam1(p, g_in[i], m, v, a);
@@ -141,15 +146,15 @@ __device__ __forceinline__ void rope1(float x0, float x1, float c, float s, floa
 }
 #pragma clang fp contract(on)
 
-// grid: (ceil(s4 / (kBlock*kRopeUnroll)), D/2).  Row d of the lower half pairs with row
+// grid: (ceil(s4 / (kRopeBlock*kRopeUnroll)), D/2).  Row d of the lower half pairs with row
 // d + D/2 of the upper half; cos/sin rows are shared by both outputs.
-__global__ __launch_bounds__(kBlock) void rope_vec_kernel(const floatx4* __restrict__ x,
+__global__ __launch_bounds__(kRopeBlock) void rope_vec_kernel(const floatx4* __restrict__ x,
                                                           const floatx4* __restrict__ cs,
                                                           const floatx4* __restrict__ sn,
                                                           floatx4* __restrict__ out,
                                                           int64_t half, int64_t s4) {
   const int64_t d = blockIdx.y;
-  const int64_t base = (int64_t)blockIdx.x * (kBlock * kRopeUnroll) + threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * (kRopeBlock * kRopeUnroll) + threadIdx.x;
   const floatx4* x0p = x + d * s4;
   const floatx4* x1p = x + (d + half) * s4;
   const floatx4* cp = cs + d * s4;
@@ -159,7 +164,7 @@ __global__ __launch_bounds__(kBlock) void rope_vec_kernel(const floatx4* __restr
   floatx4 a[kRopeUnroll], b[kRopeUnroll], c[kRopeUnroll], s[kRopeUnroll];
 #pragma unroll
   for (int u = 0; u < kRopeUnroll; ++u) {
-    const int64_t i = base + (int64_t)u * kBlock;
+    const int64_t i = base + (int64_t)u * kRopeBlock;
     if (i < s4) {
       a[u] = __builtin_nontemporal_load(x0p + i);
       b[u] = __builtin_nontemporal_load(x1p + i);
@@ -169,7 +174,7 @@ __global__ __launch_bounds__(kBlock) void rope_vec_kernel(const floatx4* __restr
   }
 #pragma unroll
   for (int u = 0; u < kRopeUnroll; ++u) {
-    const int64_t i = base + (int64_t)u * kBlock;
+    const int64_t i = base + (int64_t)u * kRopeBlock;
     if (i < s4) {
       floatx4 r0, r1;
 #pragma unroll
@@ -185,11 +190,11 @@ __global__ __launch_bounds__(kBlock) void rope_vec_kernel(const floatx4* __restr
   }
 }
 
-__global__ __launch_bounds__(kBlock) void rope_scalar_kernel(const float* x, const float* cs,
+__global__ __launch_bounds__(kRopeBlock) void rope_scalar_kernel(const float* x, const float* cs,
                                                              const float* sn, float* out,
                                                              int64_t half, int64_t s) {
   const int64_t d = blockIdx.y;
-  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t i = (int64_t)blockIdx.x * kRopeBlock + threadIdx.x;
   if (i >= s) return;
   float o0, o1;
   rope1(x[d * s + i], x[(d + half) * s + i], cs[d * s + i], sn[d * s + i], o0, o1);
@@ -268,23 +273,23 @@ extern "C" int kda_adamw_f32(const float* param_in, const float* grad, const flo
     const int64_t n4 = n / 4;
     vec_end = n4 * 4;
     if (n4 > 0) {
-      const int64_t per_block = (int64_t)kBlock * kAdamUnroll;
+      const int64_t per_block = (int64_t)kAdamBlock * kAdamUnroll;
       if (blocks_for(n4, per_block) > 0x7fffffffu)
         return set_error(KDA_ERR_UNSUPPORTED, "adamw: n=%lld too large", (long long)n);
       auto P = [](const float* q) { return reinterpret_cast<const floatx4*>(q); };
       auto Q = [](float* q) { return reinterpret_cast<floatx4*>(q); };
       if (moments)
-        hipLaunchKernelGGL(adamw_vec_kernel<true>, dim3(blocks_for(n4, per_block)), dim3(kBlock), 0,
+        hipLaunchKernelGGL(adamw_vec_kernel<true>, dim3(blocks_for(n4, per_block)), dim3(kAdamBlock), 0,
                            st, P(param_in), P(grad), P(m_in), P(v_in), Q(param_out), Q(m_out),
                            Q(v_out), n4, a);
       else
-        hipLaunchKernelGGL(adamw_vec_kernel<false>, dim3(blocks_for(n4, per_block)), dim3(kBlock),
+        hipLaunchKernelGGL(adamw_vec_kernel<false>, dim3(blocks_for(n4, per_block)), dim3(kAdamBlock),
                            0, st, P(param_in), P(grad), P(m_in), P(v_in), Q(param_out), nullptr,
                            nullptr, n4, a);
     }
   }
   if (vec_end < n)
-    hipLaunchKernelGGL(adamw_scalar_kernel, dim3(blocks_for(n - vec_end, kBlock)), dim3(kBlock), 0,
+    hipLaunchKernelGGL(adamw_scalar_kernel, dim3(blocks_for(n - vec_end, kAdamBlock)), dim3(kAdamBlock), 0,
                        st, param_in, grad, m_in, v_in, param_out, m_out, v_out, vec_end, n, a);
   return check_launch("adamw");
 }
@@ -305,14 +310,14 @@ extern "C" int kda_rope_f32(const float* x, const float* cos_t, const float* sin
                    aligned16(out);
   if (vec) {
     const int64_t s4 = s / 4;
-    hipLaunchKernelGGL(rope_vec_kernel, dim3(blocks_for(s4, kBlock * kRopeUnroll), (unsigned)half),
-                       dim3(kBlock), 0, st, reinterpret_cast<const floatx4*>(x),
+    hipLaunchKernelGGL(rope_vec_kernel, dim3(blocks_for(s4, kRopeBlock * kRopeUnroll), (unsigned)half),
+                       dim3(kRopeBlock), 0, st, reinterpret_cast<const floatx4*>(x),
                        reinterpret_cast<const floatx4*>(cos_t),
                        reinterpret_cast<const floatx4*>(sin_t), reinterpret_cast<floatx4*>(out), half,
                        s4);
   } else {
-    hipLaunchKernelGGL(rope_scalar_kernel, dim3(blocks_for(s, kBlock), (unsigned)half),
-                       dim3(kBlock), 0, st, x, cos_t, sin_t, out, half, s);
+    hipLaunchKernelGGL(rope_scalar_kernel, dim3(blocks_for(s, kRopeBlock), (unsigned)half),
+                       dim3(kRopeBlock), 0, st, x, cos_t, sin_t, out, half, s);
   }
   return check_launch("rope");
 }
