@@ -357,8 +357,8 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU; the operators are single-GPU kernels "
-              "(multi-GPU sharding is described in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py: measures one GPU only; the operators are single-GPU kernels "
+              "with no collective step. Run with --gpus 1.", file=sys.stderr)
         return 2
 
     import torch

@@ -6,8 +6,8 @@ the bf16 / relative-L2 helpers of its offline simulators.  Each function cites
 the reference file:line it follows.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import it, and only as the checker (or, in bench.py, as the
-timed host-CPU baseline).  The product (``kda-for-trainium_amd/``) never imports
+``bench.py`` may import it, and only as the reference that device results are
+compared against (or, in bench.py, as the timed host-CPU baseline).  The product (``kda-for-trainium_amd/``) never imports
 it and has no CPU fallback.
 
 How each function is pinned (i.e. checked against something other than a
