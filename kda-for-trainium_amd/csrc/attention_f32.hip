@@ -16,9 +16,10 @@
 // v's and p's at the end.  On the NKIBench inputs this matches fp64 attention
 // as closely as the fp32 reference does (rel-L2 5.6e-7 against 5.4e-7).
 //
-// Pre-passes (q_split_kernel, k_split_kernel, v_split_kernel) write the limb
-// planes in the input layout [B][S][H][D] plus the scales into the caller's
-// workspace.
+// Pre-passes (k_split_kernel, v_split_kernel) write the K and V limb planes in
+// the input layout [B][S][Hkv][D] plus their scales into the caller's
+// workspace; q is split by the attention kernel itself as it loads it (once per
+// wave; a q pre-pass cost 11 us of 373 at the NKIBench shape).
 //
 // Work decomposition: one workgroup = (batch b, kv head, block of 128 queries);
 // its 8 waves are the 2 query heads of that kv head x 4 quarters of the query
@@ -97,24 +98,6 @@ __device__ __forceinline__ float block_max(float x, float* red) {
   return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-// q rows (128 floats each, `rows` = B*S*Hq of them in [B][S][Hq] order): limbs of
-// q * 2^(kTopExp - e) and qinv[row] = 2^(e - kTopExp).  32 threads per row.
-__global__ __launch_bounds__(kSplitThreads) void q_split_kernel(const float* __restrict__ q,
-                                                                _Float16* __restrict__ q0,
-                                                                _Float16* __restrict__ q1,
-                                                                float* __restrict__ qinv,
-                                                                int64_t rows) {
-  const int64_t row = (int64_t)blockIdx.x * (kSplitThreads / 32) + (threadIdx.x >> 5);
-  const int t = threadIdx.x & 31;
-  if (row >= rows) return;   // whole 32-lane groups leave together
-  const floatx4 x = *reinterpret_cast<const floatx4*>(q + row * kD + 4 * t);
-  float mx = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
-  for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
-  const int e = top_exponent(mx);
-  store_limbs4(x, pow2(kTopExp - e), q0 + row * kD + 4 * t, q1 + row * kD + 4 * t);
-  if (t == 0) qinv[row] = pow2(e - kTopExp);
-}
-
 // One workgroup per (64-key tile, batch x kv head): limbs of the K tile scaled
 // by its own power of two (kinv[bh][tile]), and the V tile's largest |value|
 // (vtmax[bh][tile]) for the per-head V scale.
@@ -184,10 +167,9 @@ __global__ __launch_bounds__(kSplitThreads) void v_split_kernel(const float* __r
 }
 
 struct Args {
-  const _Float16 *q0, *q1;   // [B][S][Hq][D]
+  const float* q;            // [B][S][Hq][D], fp32 (split in the kernel)
   const _Float16 *k0, *k1;   // [B][S][Hkv][D]
   const _Float16 *v0, *v1;
-  const float* qinv;         // [B][S][Hq]
   const float* kinv;         // [B*Hkv][nt]
   const float* vinv;         // [B*Hkv]
   float* out;
@@ -235,19 +217,40 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_f32_kernel(Args p) {
   const int w0 = q0 + (wave / kGroup) * kWaveRows;   // this wave's first query row
 
   // ---- Q fragments (MFMA B operand, two limbs): row w0 + 16it + l16, d = 32dc + 8g .. +7.
+  // Each row is scaled by 2^(kTopExp - e), e the exponent of its largest |value|
+  // (the four lanes of a row hold its 128 values), and split into fp16 limbs
+  // here: q is read once per wave, so no pre-pass is needed for it.
   // Rows past the sequence read the last row and are never stored.
   half8 qf[kIT][4][2];
-  float rowc[kIT];   // scale_log2 * qinv[row]
+  float rowc[kIT];   // scale_log2 * 2^(e - kTopExp)
 #pragma unroll
   for (int it = 0; it < kIT; ++it) {
     const int row = min(w0 + it * 16 + l16, p.seq - 1);
-    const int64_t qoff = (((int64_t)b * p.seq + row) * p.hq + h) * kD;
+    const float* qr = p.q + (((int64_t)b * p.seq + row) * p.hq + h) * kD + g * 8;
+    floatx4 x[4][2];
+    float mx = 0.f;
 #pragma unroll
-    for (int dc = 0; dc < 4; ++dc) {
-      qf[it][dc][0] = *reinterpret_cast<const half8*>(p.q0 + qoff + dc * 32 + g * 8);
-      qf[it][dc][1] = *reinterpret_cast<const half8*>(p.q1 + qoff + dc * 32 + g * 8);
-    }
-    rowc[it] = p.scale_log2 * p.qinv[((int64_t)b * p.seq + row) * p.hq + h];
+    for (int dc = 0; dc < 4; ++dc)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        x[dc][hh] = *reinterpret_cast<const floatx4*>(qr + dc * 32 + hh * 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) mx = fmaxf(mx, fabsf(x[dc][hh][e]));
+      }
+    const int ex = top_exponent(row_max4(mx));
+    const float sc = pow2(kTopExp - ex);
+#pragma unroll
+    for (int dc = 0; dc < 4; ++dc)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          _Float16 h0, h1;
+          limbs2(x[dc][hh][e] * sc, h0, h1);
+          qf[it][dc][0][hh * 4 + e] = h0;
+          qf[it][dc][1][hh * 4 + e] = h1;
+        }
+    rowc[it] = p.scale_log2 * pow2(ex - kTopExp);
   }
   floatx4 o[kIT][8];
   float m[kIT], l[kIT];
@@ -439,8 +442,8 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_f32_kernel(Args p) {
 
 // Workspace layout shared by the size query and the entry point.
 struct Plan {
-  _Float16 *q0, *q1, *k0, *k1, *v0, *v1;
-  float *qinv, *kinv, *vtmax, *vinv;
+  _Float16 *k0, *k1, *v0, *v1;
+  float *kinv, *vtmax, *vinv;
   int64_t bytes;
 };
 Plan plan(void* ws, int64_t batch, int64_t seq, int64_t hq, int64_t hkv) {
@@ -452,15 +455,13 @@ Plan plan(void* ws, int64_t batch, int64_t seq, int64_t hq, int64_t hkv) {
     used = off + bytes;
     return base ? base + off : nullptr;
   };
-  const int64_t nq = batch * seq * hq * kD, nk = batch * seq * hkv * kD;
+  (void)hq;
+  const int64_t nk = batch * seq * hkv * kD;
   const int64_t nt = (seq + kBN - 1) / kBN;
-  pl.q0 = reinterpret_cast<_Float16*>(take(nq * 2));
-  pl.q1 = reinterpret_cast<_Float16*>(take(nq * 2));
   pl.k0 = reinterpret_cast<_Float16*>(take(nk * 2));
   pl.k1 = reinterpret_cast<_Float16*>(take(nk * 2));
   pl.v0 = reinterpret_cast<_Float16*>(take(nk * 2));
   pl.v1 = reinterpret_cast<_Float16*>(take(nk * 2));
-  pl.qinv = reinterpret_cast<float*>(take(batch * seq * hq * 4));
   pl.kinv = reinterpret_cast<float*>(take(batch * hkv * nt * 4));
   pl.vtmax = reinterpret_cast<float*>(take(batch * hkv * nt * 4));
   pl.vinv = reinterpret_cast<float*>(take(batch * hkv * 4));
@@ -505,18 +506,14 @@ extern "C" int kda_gqa_fwd_f32(const float* q, const float* k, const float* v, f
     return set_error(KDA_ERR_INVALID_ARG, "%s: output strides must be multiples of 4", what);
   const int64_t nt = (seq + kBN - 1) / kBN;
   const int64_t nblocks = ((seq + kBM - 1) / kBM) * batch * hkv;
-  const int64_t qrows = batch * seq * hq;
   if (nblocks > 0x7fffffff || seq > (1 << 24) || batch * hkv > 65535 || nt > 0x7fffffff ||
-      (qrows + 7) / 8 > 0x7fffffff || batch * seq * hq * kD * 2 > ((int64_t)1 << 32))
+      batch * seq * hq * kD * 2 > ((int64_t)1 << 32))
     return set_error(KDA_ERR_UNSUPPORTED, "%s: problem too large", what);
   const Plan pl = plan(workspace, batch, seq, hq, hkv);
   if (!workspace || !aligned16(workspace) || workspace_bytes < pl.bytes)
     return set_error(KDA_ERR_INVALID_ARG, "%s: workspace must be 16-byte aligned and >= %lld bytes",
                      what, (long long)pl.bytes);
   hipStream_t st = as_stream(stream);
-  hipLaunchKernelGGL(q_split_kernel, dim3((unsigned)((qrows + 7) / 8)), dim3(kSplitThreads), 0, st,
-                     q, pl.q0, pl.q1, pl.qinv, qrows);
-  if (int rc = check_launch(what)) return rc;
   const dim3 kv_grid((unsigned)nt, (unsigned)(batch * hkv));
   hipLaunchKernelGGL(k_split_kernel, kv_grid, dim3(kSplitThreads), 0, st, k, v, pl.k0, pl.k1,
                      pl.kinv, pl.vtmax, (int)seq, (int)hkv);
@@ -526,13 +523,11 @@ extern "C" int kda_gqa_fwd_f32(const float* q, const float* k, const float* v, f
   if (int rc = check_launch(what)) return rc;
 
   Args a;
-  a.q0 = pl.q0;
-  a.q1 = pl.q1;
+  a.q = q;
   a.k0 = pl.k0;
   a.k1 = pl.k1;
   a.v0 = pl.v0;
   a.v1 = pl.v1;
-  a.qinv = pl.qinv;
   a.kinv = pl.kinv;
   a.vinv = pl.vinv;
   a.out = out;
