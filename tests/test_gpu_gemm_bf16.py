@@ -55,7 +55,9 @@ def test_rmsnorm_matmul_config_full_size_all_seeds(dev):
 
 
 @pytest.mark.parametrize("dims", [dict(M=256, K=64, N=128), dict(M=77, K=136, N=56),
-                                  dict(M=1, K=8, N=8), dict(M=513, K=1000, N=264)])
+                                  dict(M=1, K=8, N=8), dict(M=513, K=1000, N=264),
+                                  # K past what the norm pre-pass holds in registers (4096)
+                                  dict(M=40, K=5000, N=72)])
 def test_rmsnorm_matmul_ragged(dev, dims):
     d = oi.draw("rmsnorm_matmul_cfg", 3, dims=dims)
     got = ops.rmsnorm_matmul(to_dev(d["x"], dev, BF), to_dev(d["w"], dev, BF),
