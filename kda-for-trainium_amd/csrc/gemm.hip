@@ -564,6 +564,27 @@ __global__ __launch_bounds__(256) void split_f32_kernel(const floatx4* __restric
   }
 }
 
+// Sum of S fp32 split-K partial planes [S][n] (in order of the planes), split
+// into bf16 (hi, lo) planes like split_f32_kernel.
+__global__ __launch_bounds__(256) void sum_split_f32_kernel(const floatx4* __restrict__ part, int parts,
+                                                            u32x2* __restrict__ hi, u32x2* __restrict__ lo,
+                                                            int64_t n4) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+    floatx4 v = __builtin_nontemporal_load(part + i);
+    for (int z = 1; z < parts; ++z) v += __builtin_nontemporal_load(part + z * n4 + i);
+    uint32_t h[4];
+    float l[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      h[e] = f32_to_bf16_bits(v[e]);
+      l[e] = v[e] - bf16_bits_to_f32(h[e]);
+    }
+    hi[i] = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    lo[i] = u32x2{f32_to_bf16_bits(l[0]) | (f32_to_bf16_bits(l[1]) << 16),
+                  f32_to_bf16_bits(l[2]) | (f32_to_bf16_bits(l[3]) << 16)};
+  }
+}
+
 // x [K][M] fp32 -> bf16 hi/lo planes of x^T, [M][K] (K-contiguous, so the GEMM
 // reads A with ds_read_b128 fragments instead of transposed LDS reads).  One
 // workgroup per 64 x 64 block through LDS; M % 8 == 0, K % 8 == 0.
@@ -952,10 +973,20 @@ SplitPlan plan_split(Carve& c, int64_t count_a, int64_t count_b) {
   s.bl = c.take<uint16_t>(count_b);
   return s;
 }
+// K-chunks for the small GEMM t = x @ a [M, R]: its 256x128 tiles would occupy few
+// CUs (4096 x 128: 16 tiles), so K is split into up to 16 chunks run as a batch
+// into fp32 partials (each chunk a whole number of 64-deep k-tiles).
+int lora_t_parts(int64_t m, int64_t k, int64_t r) {
+  const int64_t tiles = ((m + 255) / 256) * ((r + 127) / 128);
+  int parts = 1;
+  while (parts < 16 && tiles * parts * 2 <= device_cu_count() && k % (parts * 2 * 64) == 0) parts *= 2;
+  return parts;
+}
 struct LoraPlan {
   SplitPlan xw;        // x [M,K], w [K,N]
   uint16_t *ah, *al;   // a [K,R]
-  float* t;            // x@a [M,R]
+  float* t;            // x@a [M,R], as `parts` split-K partials [parts][M][R]
+  int parts;
   uint16_t *th, *tl;   // split t
   uint16_t *bh, *bl;   // b [R,N]
 };
@@ -964,7 +995,8 @@ LoraPlan plan_lora(Carve& c, int64_t m, int64_t k, int64_t n, int64_t r) {
   p.xw = plan_split(c, m * k, k * n);
   p.ah = c.take<uint16_t>(k * r);
   p.al = c.take<uint16_t>(k * r);
-  p.t = c.take<float>(m * r);
+  p.parts = r > 0 ? lora_t_parts(m, k, r) : 1;
+  p.t = c.take<float>(p.parts * m * r);
   p.th = c.take<uint16_t>(m * r);
   p.tl = c.take<uint16_t>(m * r);
   p.bh = c.take<uint16_t>(r * n);
@@ -1298,10 +1330,27 @@ extern "C" int kda_lora_f32(const float* x, const float* w, const float* a, cons
     if (int rc = split(a, k * r, lp.ah, lp.al, st, what)) return rc;
     if (int rc = split(b, r * n, lp.bh, lp.bl, st, what)) return rc;
     // t = x @ a  [M, R]
-    Params pt = make_params(m, r, lp.t, r);
-    add_split_segs(pt, lp.xw.ah, lp.xw.al, k, lp.ah, lp.al, r, k);
-    if (int rc = launch_auto<true, Epi::kStoreF32>(pt, 1, st, "lora_f32(x@a)")) return rc;
-    if (int rc = split(lp.t, m * r, lp.th, lp.tl, st, what)) return rc;
+    if (lp.parts > 1 && (m * r) % 4 == 0) {
+      const int64_t kc = k / lp.parts;
+      Params pt = make_params(m, r, lp.t, r);
+      add_split_segs(pt, lp.xw.ah, lp.xw.al, k, lp.ah, lp.al, r, kc);
+      pt.batch_a = kc;       // chunk z: columns z*kc.. of x
+      pt.batch_b = kc * r;   //          rows z*kc.. of a
+      pt.batch_c = m * r;    //          partial plane z
+      if (int rc = launch<256, 128, 1, true, Epi::kStoreF32, 64, 2>(pt, lp.parts, st, "lora_f32(x@a, split-K)"))
+        return rc;
+      const int64_t n4 = m * r / 4;
+      const int64_t blocks = std::min<int64_t>((n4 + 255) / 256, (int64_t)device_cu_count() * 16);
+      hipLaunchKernelGGL(sum_split_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                         reinterpret_cast<const floatx4*>(lp.t), lp.parts, reinterpret_cast<u32x2*>(lp.th),
+                         reinterpret_cast<u32x2*>(lp.tl), n4);
+      if (int rc = check_launch("lora_f32(t sum)")) return rc;
+    } else {
+      Params pt = make_params(m, r, lp.t, r);
+      add_split_segs(pt, lp.xw.ah, lp.xw.al, k, lp.ah, lp.al, r, k);
+      if (int rc = launch_auto<true, Epi::kStoreF32>(pt, 1, st, "lora_f32(x@a)")) return rc;
+      if (int rc = split(lp.t, m * r, lp.th, lp.tl, st, what)) return rc;
+    }
   }
   // out = x @ w + t @ b in one accumulation
   Params p = make_params(m, n, out, n);

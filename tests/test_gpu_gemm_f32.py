@@ -50,7 +50,9 @@ SMALL = {
     "matmul": [dict(M=256, K=64, N=256), dict(M=37, K=96, N=40), dict(M=300, K=160, N=264),
                dict(M=1, K=32, N=8)],
     "transpose_matmul": [dict(M=256, K=64, N=256), dict(M=40, K=96, N=72), dict(M=264, K=160, N=136)],
-    "lora": [dict(M=256, K=64, N=256, R=32), dict(M=77, K=96, N=136, R=64)],
+    "lora": [dict(M=256, K=64, N=256, R=32), dict(M=77, K=96, N=136, R=64),
+             # x@a split along K into 16 and into 2 fp32 partials
+             dict(M=512, K=1024, N=256, R=128), dict(M=300, K=640, N=200, R=64)],
     "rmsnorm_matmul": [dict(M=256, K=128, N=256), dict(M=50, K=96, N=72)],
     "add_rmsnorm_matmul": [dict(M=256, K=128, N=256), dict(M=50, K=96, N=72)],
     "matmul_add_rmsnorm": [dict(M=256, K=128, N=256), dict(M=50, K=96, N=200), dict(M=300, K=64, N=520)],
