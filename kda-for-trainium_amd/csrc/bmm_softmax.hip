@@ -19,10 +19,13 @@
 // Work decomposition.  One workgroup = 256 rows of one batch (8 waves x 2 x 16
 // rows); it streams the N axis in 64-column tiles of rhs^T (two fp16 limb
 // planes [N][K] and the tile scales, made by split_transpose_kernel), DMA'd
-// global->LDS into a ring of three buffers shared by the 8 waves.  Two passes
-// over N:
+// global->LDS into a ring of three buffers shared by the 8 waves.  Each 16-row
+// group makes two passes over N:
 //   pass 0: online row max and sum of 2^(s - max) (flash-softmax statistics);
 //   pass 1: recompute the scores and write 2^(s - max) / sum once.
+// The two groups of a wave run one pass apart over three sweeps of the tiles
+// (group 0's statistics; group 0's stores with group 1's statistics; group 1's
+// stores), so that stores are in flight during two of the three sweeps.
 // The output (4 bytes per element) is written exactly once; recomputing the
 // K = 64 scores is cheaper than a second pass over the output in HBM.  Scores
 // are kept in log2 units (lhs is multiplied by log2(e) before the split), so
@@ -34,6 +37,8 @@
 // row r at c ^ (r & 7)); lane l then holds row l % 16, columns 4*(l/16) .. +3 of
 // each 16x16 block.
 #include <math.h>
+
+#include <type_traits>
 
 #include "common.h"
 #include "lanes.h"
@@ -55,7 +60,7 @@ constexpr int kPlaneBytes = kCols * kK * 2;               // one limb plane of a
 constexpr int kTileBytes = kLimbs * kPlaneBytes;          // 16 KiB
 constexpr int kDmaPerWave = kTileBytes / 1024 / kWaves;   // 2
 constexpr int kStages = 3;                                // tile ring depth
-constexpr int kStores = 4 * kGroups;                      // store instructions per wave and tile
+constexpr int kStores = 4;                                // store instructions per wave and storing step (one group)
 constexpr int kTopExp = 13;                               // largest |scaled value| in [2^13, 2^14)
 constexpr float kLog2e = 1.44269504088896341f;
 #define KDA_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
@@ -225,12 +230,14 @@ __global__ __launch_bounds__(kThreads, 1) void bmm_softmax_kernel(
 
   // Scores of the tile in buffer `buf`: 2 x 4 independent 16x16 blocks, issued
   // term by term so consecutive MFMAs never depend on each other.
-  auto scores = [&](int buf, Scores& s) {
+  auto scores = [&](int buf, Scores& s, auto gmask) {
+    constexpr int GM = decltype(gmask)::value;   // bit g: compute group g
     const uint8_t* tile = &lds[buf][0];
 #pragma unroll
     for (int g = 0; g < kGroups; ++g)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) s[g][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < 4; ++j)
+        if (GM & (1 << g)) s[g][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
       const int c = kh * 4 + (lane >> 4);
@@ -250,7 +257,7 @@ __global__ __launch_bounds__(kThreads, 1) void bmm_softmax_kernel(
         for (int g = 0; g < kGroups; ++g)
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            s[g][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bt[j][kTerm[t][0]], a[g][kh][kTerm[t][1]],
+            if (GM & (1 << g)) s[g][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bt[j][kTerm[t][0]], a[g][kh][kTerm[t][1]],
                                                              s[g][j], 0, 0, 0);
     }
   };
@@ -259,51 +266,54 @@ __global__ __launch_bounds__(kThreads, 1) void bmm_softmax_kernel(
   float m_run[kGroups], l_run[kGroups], inv_l[kGroups];
 #pragma unroll
   for (int g = 0; g < kGroups; ++g) m_run[g] = -INFINITY, l_run[g] = 0.f;
-  auto stats = [&](const Scores& s, float ts) {
+  auto stats = [&](const Scores& s, float ts, auto gc) {
+    constexpr int g = decltype(gc)::value;
+    const float c = row_scale[g] * ts;
+    float mx = s[g][0][0];
 #pragma unroll
-    for (int g = 0; g < kGroups; ++g) {
-      const float c = row_scale[g] * ts;
-      float mx = s[g][0][0];
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[g][j][r]);
+    const float m_new = fmaxf(m_run[g], row_max4(mx) * c);
+    float sum = 0.f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[g][j][r]);
-      const float m_new = fmaxf(m_run[g], row_max4(mx) * c);
-      float sum = 0.f;
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sum += __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][j][r], c, -m_new));
-      l_run[g] = l_run[g] * __builtin_amdgcn_exp2f(m_run[g] - m_new) + sum;
-      m_run[g] = m_new;
-    }
+      for (int r = 0; r < 4; ++r) sum += __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][j][r], c, -m_new));
+    l_run[g] = l_run[g] * __builtin_amdgcn_exp2f(m_run[g] - m_new) + sum;
+    m_run[g] = m_new;
   };
   // pass 1: normalised probabilities of column tile col, stored directly
-  auto probs = [&](const Scores& s, float ts, int col) {
+  auto probs = [&](const Scores& s, float ts, int col, auto gc) {
+    constexpr int g = decltype(gc)::value;
+    const float c = row_scale[g] * ts;
 #pragma unroll
-    for (int g = 0; g < kGroups; ++g) {
-      const float c = row_scale[g] * ts;
+    for (int j = 0; j < 4; ++j) {
+      floatx4 p;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        floatx4 p;
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][j][r], c, -m_run[g])) * inv_l[g];
-        *reinterpret_cast<floatx4*>(orow[g] + col * kCols + j * 16) = p;
-      }
+      for (int r = 0; r < 4; ++r)
+        p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][j][r], c, -m_run[g])) * inv_l[g];
+      *reinterpret_cast<floatx4*>(orow[g] + col * kCols + j * 16) = p;
     }
   };
 
-  // Software pipeline over the 2*nt steps (step t = column tile (t + rot) % nt,
-  // pass t / nt), ring of kStages LDS buffers.  Iteration t: wait for this
-  // wave's DMA of step t+1, barrier (step t+1 visible everywhere; buffer t %
-  // kStages, last read by the MFMAs of step t one iteration ago, is free), issue
-  // the DMA of step t+3 into it, then the MFMAs of step t+1 interleaved with the
-  // softmax work of step t, whose scores the previous iteration produced.
-  // vmcnt counts loads and stores together and retires in issue order: after
-  // DMA(t+1) come the stores of iteration t-2, DMA(t+2) and the stores of
-  // iteration t-1, which may stay in flight.
-  const int total = 2 * nt;
+  // The two 16-row groups of every wave run one pass apart, so that the stores of
+  // one group overlap the statistics pass of the other instead of every
+  // workgroup storing only in its second half:
+  //   steps [0, nt):      group 0 pass 0 (statistics)
+  //   steps [nt, 2nt):    group 0 pass 1 (probabilities, stored) + group 1 pass 0
+  //   steps [2nt, 3nt):   group 1 pass 1
+  // (step t = column tile (t + rot) % nt).  Software pipeline over the 3*nt steps,
+  // ring of kStages LDS buffers.  Iteration t: wait for this wave's DMA of step
+  // t+1, barrier (step t+1 visible everywhere; buffer t % kStages, last read by
+  // the MFMAs of step t one iteration ago, is free), issue the DMA of step t+3
+  // into it, then the MFMAs of step t+1 (only the groups it needs) interleaved
+  // with the softmax work of step t, whose scores the previous iteration
+  // produced.  vmcnt counts loads and stores together and retires in issue order:
+  // after DMA(t+1) come the stores of iteration t-2, DMA(t+2) and the stores of
+  // iteration t-1, which may stay in flight (every step from nt on stores one
+  // group: kStores instructions).
+  const int total = 3 * nt;
   auto col = [&](int t) { return (t + rot) % nt; };
   auto dma_after = [&](int t) {   // operations allowed in flight at iteration t
     return (t - 2 >= nt ? kStores : 0) + (t + 2 < total ? kDmaPerWave : 0) + (t - 1 >= nt ? kStores : 0);
@@ -322,66 +332,82 @@ __global__ __launch_bounds__(kThreads, 1) void bmm_softmax_kernel(
     if (t + 3 < total) issue(col(t + 3), (t + 3) % kStages);
   };
 
+  using G0 = std::integral_constant<int, 0>;
+  using G1 = std::integral_constant<int, 1>;
+  using M0 = std::integral_constant<int, 1>;    // group 0 only
+  using M1 = std::integral_constant<int, 2>;    // group 1 only
+  using M01 = std::integral_constant<int, 3>;   // both groups
+
   issue(col(0), 0);
-  issue(col(1), 1);   // total >= 2
-  if (total > 2) {
-    issue(col(2), 2);
-    wait_vmcnt<2 * kDmaPerWave>();
-  } else {
-    wait_vmcnt<kDmaPerWave>();
-  }
+  issue(col(1), 1);
+  issue(col(2), 2);   // total >= 3
+  wait_vmcnt<2 * kDmaPerWave>();
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   Scores sa, sb;
-  scores(0, sa);
+  scores(0, sa, M0{});
   float ta = tscale[col(0)], tb;
 
-  // one pipeline iteration; `cur` / `ts` hold step t, `next` / `ts_next`
-  // receive step t+1
-  auto step0 = [&](int t, const Scores& cur, float ts, Scores& next, float& ts_next) {
+  // One pipeline iteration of each kind; `cur` / `ts` hold step t, `next` /
+  // `ts_next` receive step t+1 (for the groups step t+1 needs: NEXT).
+  // The empty asm keeps the statistics in the iteration's block: without a use
+  // there LLVM sinks them past the next wait's branches, away from the MFMAs
+  // they should overlap.
+  // (non-generic: an asm statement naming captured arrays does not compile in a
+  // generic lambda)
+  auto pin_stats0 = [&]() { asm volatile("" ::"v"(m_run[0]), "v"(l_run[0])); };
+  auto pin_stats1 = [&]() { asm volatile("" ::"v"(m_run[1]), "v"(l_run[1])); };
+  auto step_a = [&](int t, const Scores& cur, float ts, Scores& next, float& ts_next, auto next_mask) {
     wait_step(t);
     ts_next = tscale[col(t + 1)];
-    scores((t + 1) % kStages, next);
-    stats(cur, ts);
-    interleave<48, 2>();
-    // keep the statistics in this block: without a use here LLVM sinks them
-    // past the next wait's branches, away from the MFMAs they should overlap
-#pragma unroll
-    for (int g = 0; g < kGroups; ++g) asm volatile("" ::"v"(m_run[g]), "v"(l_run[g]));
+    scores((t + 1) % kStages, next, next_mask);
+    stats(cur, ts, G0{});
+    interleave<24, 2>();
+    pin_stats0();
   };
-  auto step1 = [&](int t, const Scores& cur, float ts, Scores& next, float& ts_next) {
+  auto step_m = [&](int t, const Scores& cur, float ts, Scores& next, float& ts_next, auto next_mask) {
     wait_step(t);
     ts_next = tscale[col(t + 1)];
-    scores((t + 1) % kStages, next);
-    probs(cur, ts, col(t));
+    scores((t + 1) % kStages, next, next_mask);
+    probs(cur, ts, col(t), G0{});
+    stats(cur, ts, G1{});
     interleave<48, 2>();
+    pin_stats1();
   };
+  auto step_c = [&](int t, const Scores& cur, float ts, Scores& next, float& ts_next, auto next_mask) {
+    wait_step(t);
+    ts_next = tscale[col(t + 1)];
+    scores((t + 1) % kStages, next, next_mask);
+    probs(cur, ts, col(t), G1{});
+    interleave<24, 2>();
+  };
+  // `count` iterations from step t, alternating the score buffers; the current
+  // step's scores are in sa on entry and on exit
   int t = 0;
-  for (; t + 1 < nt; t += 2) {
-    step0(t, sa, ta, sb, tb);
-    step0(t + 1, sb, tb, sa, ta);
-  }
-  if (t < nt) {   // odd nt: one more statistics step, then bring its output to sa
-    step0(t, sa, ta, sb, tb);
-    ++t;
+  auto run = [&](auto&& step, int count, auto next_mask) {
+    int i = 0;
+    for (; i + 1 < count; i += 2, t += 2) {
+      step(t, sa, ta, sb, tb, next_mask);
+      step(t + 1, sb, tb, sa, ta, next_mask);
+    }
+    if (i < count) {
+      step(t, sa, ta, sb, tb, next_mask);
+      ++t;
 #pragma unroll
-    for (int g = 0; g < kGroups; ++g)
+      for (int g = 0; g < kGroups; ++g)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sa[g][j] = sb[g][j];
-    ta = tb;
-  }
-#pragma unroll
-  for (int g = 0; g < kGroups; ++g) inv_l[g] = 1.0f / row_sum4(l_run[g]);
-  for (; t + 1 < total - 1; t += 2) {
-    step1(t, sa, ta, sb, tb);
-    step1(t + 1, sb, tb, sa, ta);
-  }
-  if (t < total - 1) {
-    step1(t, sa, ta, sb, tb);
-    probs(sb, tb, col(t + 1));
-  } else {
-    probs(sa, ta, col(t));
-  }
+        for (int j = 0; j < 4; ++j) sa[g][j] = sb[g][j];
+      ta = tb;
+    }
+  };
+  run(step_a, nt - 1, M0{});
+  run(step_a, 1, M01{});          // step nt (both groups) follows
+  inv_l[0] = 1.0f / row_sum4(l_run[0]);
+  run(step_m, nt - 1, M01{});
+  run(step_m, 1, M1{});           // step 2nt (group 1 only) follows
+  inv_l[1] = 1.0f / row_sum4(l_run[1]);
+  run(step_c, nt - 1, M1{});
+  probs(sa, ta, col(t), G1{});    // step 3nt - 1
 }
 
 }  // namespace bmmsm
