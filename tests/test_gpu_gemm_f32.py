@@ -81,9 +81,26 @@ def test_bmm_full_size_sampled_batches():
         torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("dims", [dict(B=3, M=256, K=64, N=256), dict(B=2, M=100, K=96, N=72)])
+@pytest.mark.parametrize("dims", [dict(B=3, M=256, K=64, N=256), dict(B=2, M=100, K=96, N=72),
+                                  dict(B=2, M=130, K=32, N=200), dict(B=1, M=17, K=64, N=8)])
 def test_bmm_small(dims):
     assert _run("bmm", ops.bmm, oo.bmm, 5, dims=dims) < GATE
+
+
+@pytest.mark.parametrize("dims", [dict(B=2, M=130, K=64, N=200), dict(B=3, M=64, K=32, N=72)])
+def test_bmm_small_k_without_workspace(dims):
+    # K <= 64 needs no workspace (fragments are split in registers): a NULL
+    # workspace is accepted and gives the same products, same gate.
+    from kda import _lib
+    d = oi.draw("bmm", 11, dims=dims)
+    lhs, rhs = to_dev(d["lhs"], "cuda"), to_dev(d["rhs"], "cuda")
+    b, m, k, n = dims["B"], dims["M"], dims["K"], dims["N"]
+    out = torch.empty((b, m, n), dtype=torch.float32, device="cuda")
+    _lib.call("kda_bmm_f32", lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), b, m, k, n, None, 0,
+              torch.cuda.current_stream().cuda_stream)
+    err = rel_l2(to_host(out), oo.bmm(d["lhs"], d["rhs"]))
+    print(f"bmm (no workspace) dims={dims} rel_l2={err:.3e}", flush=True)
+    assert err < GATE
 
 
 def test_matmul_f32_layout_identity():
