@@ -259,8 +259,9 @@ def bmm_softmax(lhs: torch.Tensor, rhs: torch.Tensor,
     """out = softmax(lhs @ rhs, axis=2) (max-shifted), lhs (B, M, K), rhs (B, K, N), fp32.
 
     K <= 64, N a multiple of 64.  One fused kernel: online row statistics, then
-    the scores are recomputed and the probabilities written once.  Scores use a
-    three-limb bf16 split of both operands (six MFMA products).
+    the scores are recomputed and the probabilities written once.  Each lhs row
+    and each 64-column rhs tile is scaled by a power of two and split into two
+    fp16 limbs; the scores are three fp16 MFMA products.
     Reference: workspaces/bmm_softmax/runs/bmm_softmax_v4.py:10-181, forward
     workspaces/bmm_softmax/docs/draft-phase1.md:14-23.
     """
