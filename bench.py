@@ -435,6 +435,10 @@ def main():
             f"frac={rl['frac']:.3f}  cpu={row.get('cpu_p50_ms')} ms")
         nki[n] = row
 
+    if not names:
+        # only NKIBench-shape operators were requested: no headline line to build
+        print(json.dumps({"nkibench": nki}), flush=True)
+        return 0
     speedups = {n: cpu[n]["p50_ms"] / results[n]["p50_ms"] for n in names if n in cpu}
     geo = harness.geomean(list(speedups.values())) if speedups else None
     dominant = max(names, key=lambda n: results[n]["p50_ms"])
