@@ -1,15 +1,18 @@
 #!/usr/bin/env python3
 """Benchmark of the five graded operator configurations on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--iters I] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--iters I] [--no-cpu] [--ledger DIR]
 
 Metric: p50 latency per op + % of HBM/MFMA roofline; geomean speedup vs host
 numpy.  For each configuration the GPU kernel is timed with HIP events on the
-stream it is launched on (p50 over --iters reps after warmup; memory-bound ops
-rotate buffer sets larger than the 256 MB Infinity Cache), and the numpy
-reference forward is timed on this host's CPU (bounded samples, scaled).  The
+stream it is launched on (p50 over --iters reps after --op-warmup calls and at
+least 0.2 s of warm-up; memory-bound ops rotate buffer sets larger than the
+256 MB Infinity Cache), and the numpy reference forward is timed on this host's
+CPU (bounded samples, scaled; p50 of 3 after one warm-up).  The same CPU leg
+checks the GPU output on its seed-0 sample against that numpy output.  The
 "step" of the driver contract is one pass over the five operators; K steps are
-timed between two device synchronisations.
+timed between two device synchronisations.  --ledger DIR appends one row per
+measured op in the reference's benchmark.csv / candidates.jsonl format.
 
 Prints exactly one JSON line on stdout; progress goes to stderr.
 """
@@ -29,6 +32,8 @@ for p in (str(ROOT), str(ROOT / "kda-for-trainium_amd")):
         sys.path.insert(0, p)
 
 METRIC = "p50 latency per op + % of HBM/MFMA roofline; geomean speedup vs host numpy"
+GATE_FP32 = 1e-5   # relative-L2 gates of the seed-0 check in the CPU-baseline leg
+GATE_BF16 = 1e-2
 
 
 def log(*a):
@@ -225,11 +230,33 @@ def _nki_shapes(name, d):
     raise KeyError(name)
 
 
-def nki_cpu_baseline(name, reps=3):
-    """The oracle (numpy) forward of an NKIBench op on this host; bmm_softmax and
-    bmm on 2 of the 16 batches, gqa_full on 2 of the 16 query heads, scaled x8.
-    Returns (ms, sample description)."""
+def _timed(fn, reps):
+    """p50 wall time in ms of fn() over `reps` calls after one warm-up call, and the
+    output of the last call."""
+    out = fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        out = fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2] * 1e3, out
+
+
+def _rel_l2(got, want):
     import numpy as np
+    g = np.asarray(got, dtype=np.float64).ravel()
+    w = np.asarray(want, dtype=np.float64).ravel()
+    den = float(np.linalg.norm(w))
+    return float(np.linalg.norm(g - w)) / den if den else float(np.linalg.norm(g))
+
+
+def nki_cpu_baseline(name, dev, reps=3):
+    """The oracle (numpy) forward of an NKIBench op on this host -- bmm_softmax and
+    bmm on 2 of the 16 batches, gqa_full on 2 of the 16 query heads, scaled x8 --
+    and, as the checker, the relative-L2 of the GPU output on the same seed-0
+    inputs.  Returns (ms, sample description, rel_l2)."""
+    import torch
+    from kda import ops
     from oracle import inputs as oi
     from oracle import ops as oo
     dims = None
@@ -237,58 +264,65 @@ def nki_cpu_baseline(name, reps=3):
     if name in ("bmm", "bmm_softmax"):
         dims, scale = dict(B=2), 8
     d = oi.draw(name, 0, dims=dims)
+    heads = [(0, 0), (0, 1)]
     if name == "gqa_full":
         scale = 8
-        fn = lambda **kw: oo.gqa(**kw, heads=[(0, 0), (0, 1)])
+        fn = lambda: oo.gqa(**d, heads=heads)
     else:
-        fn = getattr(oo, name)
-    fn(**d)
-    ts = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        fn(**d)
-        ts.append(time.perf_counter() - t0)
-    ms = sorted(ts)[len(ts) // 2] * 1e3 * scale
+        fn = lambda: getattr(oo, name)(**d)
+    ms, want = _timed(fn, reps)
+    dd = {k: (torch.from_numpy(v).to(dev) if hasattr(v, "dtype") and getattr(v, "ndim", 0) else v)
+          for k, v in d.items()}
+    got = getattr(ops, name)(**dd).float().cpu().numpy()
+    if name == "gqa_full":
+        got = got[0, [h for _, h in heads]]
     what = "heads" if name == "gqa_full" else "batches"
-    return ms, ("full shape" if scale == 1 else f"2 of 16 {what}, scaled x{scale}")
+    return (ms * scale, ("full shape" if scale == 1 else f"2 of 16 {what}, scaled x{scale}"),
+            _rel_l2(got, want))
 
 
 # ----------------------------------------------------------------- CPU baseline
 
-def cpu_baseline(name, reps=3):
-    """Times the numpy reference forward (the oracle) on this host; bounded sample,
-    scaled linearly to the full configuration.  Returns (ms, sample description)."""
-    import numpy as np
+def cpu_baseline(name, dev, reps=3):
+    """Times the numpy reference forward (the oracle) on this host on a bounded
+    sample scaled linearly to the full configuration, and, as the checker, runs the
+    GPU operator on the same seed-0 sample inputs and compares.
+    Returns (ms, sample description, rel_l2 of the GPU output)."""
+    import torch
+    from kda import ops
     from oracle import inputs as oi
     from oracle import ops as oo
-
-    def timed(fn, reps=reps):
-        fn()  # warmup
-        ts = []
-        for _ in range(reps):
-            t0 = time.perf_counter()
-            fn()
-            ts.append(time.perf_counter() - t0)
-        return sorted(ts)[len(ts) // 2] * 1e3
+    BF = torch.bfloat16
+    up = lambda a, dt=torch.float32: torch.from_numpy(a).to(dev).to(dt)
+    host = lambda t: t.float().cpu().numpy()
 
     if name == "silu":
         d = oi.draw("silu_cfg", 0)
-        return timed(lambda: oo.silu(d["x"])), "full x[2048,8192]"
+        ms, want = _timed(lambda: oo.silu(d["x"]), reps)
+        return ms, "full x[2048,8192]", _rel_l2(host(ops.silu(up(d["x"]))), want)
     if name == "rmsnorm_matmul":
         d = oi.draw("rmsnorm_matmul_cfg", 0)
-        return timed(lambda: oo.rmsnorm_matmul_gamma(**d)), "full (fp32 numpy on bf16 values)"
+        ms, want = _timed(lambda: oo.rmsnorm_matmul_gamma(**d), reps)
+        got = ops.rmsnorm_matmul(up(d["x"], BF), up(d["w"], BF), gamma=up(d["gamma"], BF), eps=d["eps"])
+        return ms, "full (fp32 numpy on bf16 values)", _rel_l2(host(got), want)
     if name == "swiglu":
         d = oi.draw("swiglu_cfg", 0)
-        return timed(lambda: oo.swiglu(**d)), "full (fp32 numpy on bf16 values)"
+        ms, want = _timed(lambda: oo.swiglu(**d), reps)
+        got = ops.swiglu(*(up(d[k], BF) for k in ("x", "w_up", "w_down", "w_gate")))
+        return ms, "full (fp32 numpy on bf16 values)", _rel_l2(host(got), want)
     if name == "adamw":
         frac = 8
         d = oi.draw("adamw_cfg", 0, dims=dict(N=(1 << 27) // frac))
-        ms = timed(lambda: oo.adamw_step(d["param"], d["grad"], d["m"], d["v"], **oi.ADAMW_CFG))
-        return ms * frac, f"n=2^24 (1/{frac} of the buffer), scaled x{frac}"
+        ms, want = _timed(lambda: oo.adamw_step(d["param"], d["grad"], d["m"], d["v"], **oi.ADAMW_CFG), reps)
+        p, g, m, v = (up(d[k]) for k in ("param", "grad", "m", "v"))
+        ops.adamw_step_(p, g, m, v, **oi.ADAMW_CFG)
+        err = max(_rel_l2(host(t), w) for t, w in zip((p, m, v), want))
+        return ms * frac, f"n=2^24 (1/{frac} of the buffer), scaled x{frac}", err
     if name == "gqa":
         d = oi.draw("gqa_cfg", 0, dims=dict(B=1, HQ=4, HKV=1))
-        ms = timed(lambda: oo.gqa(d["q"], d["k"], d["v"], causal=True), reps=1)
-        return ms * 32, "one (batch, kv-head) group of 4 query heads (1/32), scaled x32"
+        ms, want = _timed(lambda: oo.gqa(d["q"], d["k"], d["v"], causal=True), reps)
+        got = ops.gqa(*(up(d[k], BF) for k in ("q", "k", "v")), causal=True)
+        return ms * 32, "one (batch, kv-head) group of 4 query heads (1/32), scaled x32", _rel_l2(host(got), want)
     raise KeyError(name)
 
 
@@ -344,7 +378,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--iters", type=int, default=50, help="timed reps per op for the p50")
+    ap.add_argument("--iters", type=int, default=100, help="timed reps per op for the p50")
+    ap.add_argument("--op-warmup", type=int, default=20,
+                    help="untimed calls per op before its timed reps (and at least 0.2 s)")
+    ap.add_argument("--ledger", default=None,
+                    help="append one row per measured op to <DIR>/<op>/benchmark.csv and "
+                         "candidates.jsonl (the reference's evidence-ledger format)")
     ap.add_argument("--ops", default=",".join(CONFIGS), help="comma-separated subset")
     ap.add_argument("--no-cpu", action="store_true", help="skip the host numpy baseline")
     ap.add_argument("--nki", default=",".join(NKIBENCH),
@@ -382,9 +421,7 @@ def main():
     results = {}
     for n in names:
         fn, _ = cases[n]
-        warm = 3 if n == "adamw" else 10
-        iters = max(5, args.iters // 2) if n == "adamw" else args.iters
-        t = harness.time_op(fn, warmup=warm, iters=iters, device=dev)
+        t = harness.time_op(fn, warmup=args.op_warmup, iters=args.iters, device=dev)
         cfg = CONFIGS[n]
         rl = harness.roofline(cfg["work"], t.p50_ms * 1e-3, cfg["bound"])
         results[n] = dict(p50_ms=t.p50_ms, p10_ms=t.p10_ms, p90_ms=t.p90_ms, mean_ms=t.mean_ms,
@@ -409,16 +446,17 @@ def main():
     if not args.no_cpu:
         for n in names:
             log(f"[bench] cpu baseline {n}")
-            ms, sample = cpu_baseline(n)
-            cpu[n] = dict(p50_ms=ms, sample=sample)
-            log(f"[bench] cpu {n:15s} p50={ms:10.1f} ms  ({sample})")
+            ms, sample, err = cpu_baseline(n, dev)
+            gate = GATE_BF16 if CONFIGS[n]["dtype"] == "bf16" else GATE_FP32
+            cpu[n] = dict(p50_ms=ms, sample=sample, rel_l2=err, passed=bool(err <= gate))
+            log(f"[bench] cpu {n:15s} p50={ms:10.1f} ms  ({sample}); GPU rel_l2 {err:.3e} (gate {gate:g})")
 
     nki = {}
     for n in [x for x in args.nki.split(",") if x]:
         cfg = NKIBENCH[n]
         log(f"[bench] nkibench {n}")
         fn, keep = make_nki_case(n, dev)
-        t = harness.time_op(fn, warmup=10, iters=max(20, args.iters // 2), device=dev)
+        t = harness.time_op(fn, warmup=args.op_warmup, iters=args.iters, device=dev)
         rl = harness.roofline(cfg["work"], t.p50_ms * 1e-3, cfg["bound"])
         row = dict(shape=cfg["desc"], p50_ms=round(t.p50_ms, 5), bound=cfg["bound"],
                    achieved=round(rl["achieved"], 1), unit=rl["unit"], roofline_frac=round(rl["frac"], 4))
@@ -429,8 +467,9 @@ def main():
         del fn, keep
         torch.cuda.empty_cache()
         if not args.no_cpu:
-            ms, sample = nki_cpu_baseline(n)
-            row.update(cpu_p50_ms=round(ms, 2), cpu_sample=sample, speedup_vs_numpy=round(ms / t.p50_ms, 1))
+            ms, sample, err = nki_cpu_baseline(n, dev)
+            row.update(cpu_p50_ms=round(ms, 2), cpu_sample=sample, speedup_vs_numpy=round(ms / t.p50_ms, 1),
+                       seed0_rel_l2=float(f"{err:.3e}"), seed0_passed=bool(err <= GATE_FP32))
         log(f"[bench] nki {n:20s} p50={t.p50_ms * 1e3:9.1f} us  {rl['achieved']:8.1f} {rl['unit']}  "
             f"frac={rl['frac']:.3f}  cpu={row.get('cpu_p50_ms')} ms")
         nki[n] = row
@@ -473,14 +512,45 @@ def main():
                         achieved=round(results[n]["roofline"]["achieved"], 1),
                         unit=results[n]["roofline"]["unit"],
                         cpu_p50_ms=(round(cpu[n]["p50_ms"], 2) if n in cpu else None),
-                        speedup_vs_numpy=(round(speedups[n], 1) if n in speedups else None))
+                        speedup_vs_numpy=(round(speedups[n], 1) if n in speedups else None),
+                        seed0_rel_l2=(float(f"{cpu[n]['rel_l2']:.3e}") if n in cpu else None),
+                        seed0_passed=(cpu[n]["passed"] if n in cpu else None))
                 for n in names},
         "nkibench": nki or None,
         "nkibench_geomean_speedup": (harness.geomean([r["speedup_vs_numpy"] for r in nki.values()])
                                      if nki and not args.no_cpu else None),
     }
+    if args.ledger:
+        write_ledger(args.ledger, results, cpu, nki, speedups)
     print(json.dumps(line), flush=True)
     return 0
+
+
+def write_ledger(root, results, cpu, nki, speedups):
+    """One ledger row per measured operator: p50, speedup over host numpy and the
+    seed-0 check of the CPU-baseline leg (seeds [0]: a bench row, not a five-seed
+    gate result)."""
+    from kda import _lib, ledger
+    cand = f"libkda.so v{_lib.version()}"
+    for n, r in results.items():
+        c = cpu.get(n, {})
+        ledger.append(root, ledger.record(
+            op=f"{n}_cfg", candidate=cand, parent="numpy-host", passed=c.get("passed", False),
+            latency_ms=r["p50_ms"], speedup=speedups.get(n), seeds=[0], verdict="bench",
+            baseline_latency_ms=c.get("p50_ms"),
+            notes=(f"{CONFIGS[n]['desc']}; roofline {r['roofline']['frac']:.3f} of {r['roofline']['bound']}; "
+                   f"seed-0 rel_l2 {c.get('rel_l2', float('nan')):.3e}; cpu sample: {c.get('sample')}"),
+            metrics={"roofline_frac": round(r["roofline"]["frac"], 4),
+                     "achieved": round(r["roofline"]["achieved"], 1), "unit": r["roofline"]["unit"]}))
+    for n, row in nki.items():
+        ledger.append(root, ledger.record(
+            op=n, candidate=cand, parent="numpy-host", passed=row.get("seed0_passed", False),
+            latency_ms=row["p50_ms"], speedup=row.get("speedup_vs_numpy"), seeds=[0], verdict="bench",
+            baseline_latency_ms=row.get("cpu_p50_ms"),
+            notes=(f"NKIBench shape {row['shape']}; roofline {row['roofline_frac']:.3f} of {row['bound']}; "
+                   f"seed-0 rel_l2 {row.get('seed0_rel_l2')}; cpu sample: {row.get('cpu_sample')}"),
+            metrics={"roofline_frac": row["roofline_frac"], "achieved": row["achieved"], "unit": row["unit"]}))
+    log(f"[bench] ledger rows appended under {root}")
 
 
 if __name__ == "__main__":

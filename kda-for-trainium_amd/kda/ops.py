@@ -35,6 +35,7 @@ __all__ = [
     "swiglu",
     "mamba",
     "gqa",
+    "gqa_full",
 ]
 
 BF16 = torch.bfloat16
@@ -421,10 +422,14 @@ def mamba(delta: torch.Tensor, u: torch.Tensor, a: torch.Tensor, b: torch.Tensor
           c: torch.Tensor) -> torch.Tensor:
     """Selective scan, fp32: delta, u (C, M); a (C, S); b, c (S, M) -> out (C, M), S <= 16.
 
-    ``dA = exp(delta*a); dBu = delta*b*u; h = dA*h + dBu; out = sum_s c*h`` sequentially
-    over M (workspaces/mamba/docs/draft-phase1.md:24-30; kernel(delta, u, a, b, c) of
-    workspaces/mamba/runs/mamba_v4_s4unroll.py:7-117).  Every step rounds as numpy does
-    (numpy's float32 exp, pairwise sum over s), so the result equals the numpy definition.
+    ``dA = exp(delta*a); dBu = delta*b*u; h = dA*h + dBu; out = sum_s c*h`` over M
+    (workspaces/mamba/docs/draft-phase1.md:24-30; kernel(delta, u, a, b, c) of
+    workspaces/mamba/runs/mamba_v4_s4unroll.py:7-117), evaluated as a chunked
+    parallel scan: 8-step chunks folded into (prod dA, h) pairs, scanned across the
+    lanes of a wave in fp64, then re-run from their entry states.  exp is numpy's
+    float32 exp bit for bit; the states are summed in order s = 0..S-1.  Within
+    ~2e-6 relative-L2 of the sequential numpy evaluation (not bit-identical: the
+    entry state of each chunk is rounded once to fp32).
     """
     for name, t in (("delta", delta), ("u", u), ("a", a), ("b", b), ("c", c)):
         _check(name, t, F32, ndim=2)
@@ -490,3 +495,15 @@ def gqa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False,
               bsz, s, hq, hkv, d, sc, 1 if causal else 0, *strides, ws.data_ptr(), ws.numel(),
               _stream(q))
     return out
+
+
+def gqa_full(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+             workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The NKIBench gqa_full forward: non-causal attention with scale 1/sqrt(D),
+    query head h reading kv head h // (Hq/Hkv), returned as (B, Hq, S, D).
+
+    q (B, S, Hq, D), k/v (B, S, Hkv, D) natural layout; the output layout is the
+    reference's ``ref[0, qh, n, d]`` (workspaces/gqa_full/docs/draft-phase1.md:41-43;
+    forward in workspaces/gqa_full/runs/offline_score_bf16_split_sim.py:100-123).
+    """
+    return gqa(q, k, v, causal=False, scale=None, out_layout="bhsd", workspace=workspace)
