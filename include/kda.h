@@ -204,9 +204,14 @@ int kda_bmm_softmax_f32(const float* lhs, const float* rhs, float* out, int64_t 
 /* Mamba selective scan, fp32:
  *   dA = exp(delta[c,m] * a[c,s]);  dBu = (delta[c,m] * b[s,m]) * u[c,m]
  *   h[c,s,m] = dA * h[c,s,m-1] + dBu  (h = 0 before m = 0);  out[c,m] = sum_s c[s,m] h[c,s,m]
- * delta, u, out [C,M]; a [C,S]; b, c [S,M]; 1 <= S <= 16.  Sequential over M per
- * (channel, state) with numpy's rounding at every step (exp as numpy's float32 exp,
- * pairwise sum over s): the result equals the numpy definition bit for bit.
+ * delta, u, out [C,M]; a [C,S]; b, c [S,M]; 1 <= S <= 16; any alignment.
+ * A chunked parallel scan: one workgroup per channel, one wave per state, 8-step
+ * chunks per lane folded into (prod dA, h) pairs and scanned across the wave in
+ * fp64, then re-run from their entry states; the states are summed in order
+ * s = 0..S-1 and exp is numpy's float32 exp bit for bit.  Not bit-identical to
+ * the sequential evaluation (each chunk's entry state is rounded once to fp32):
+ * ~2e-6 relative-L2 at C256 M7168 S16 on N(0, 0.05) inputs; bit-identical when
+ * M <= 8.  Scratch: none.
  * Replaces kernel(delta, u, a, b, c) of workspaces/mamba/runs/mamba_v4_s4unroll.py:7-117
  * (forward workspaces/mamba/docs/draft-phase1.md:24-30). */
 int kda_mamba_f32(const float* delta, const float* u, const float* a, const float* b,

@@ -39,7 +39,8 @@ PINNED_BY = {
     "gqa": "torch scaled_dot_product_attention with kv heads repeated (float64); causal row 0 == v[0]",
     "mamba": "O(M^2) closed form state_i = sum_j prod_{j<k<=i} dA_k * dBu_j (float64) on tiny "
              "shapes; reference KAT ||out||~2.055, max|out|~0.0127 at seed 42 "
-             "(workspaces/mamba/docs/draft-phase1.md:93-96)",
+             "(workspaces/mamba/docs/draft-phase1.md:93-96); the state sum is sequential in s "
+             "(bit-equal to an explicit s-loop, and differs in the last bits from a pairwise sum)",
 }
 
 
@@ -240,21 +241,23 @@ def gqa(q, k, v, causal=False, scale=None, heads=None, out_layout="bshd"):
 # ----------------------------------------------------------------- selective scan
 
 def mamba(delta, u, a, b, c):
-    """Selective scan, sequential over M
-    (workspaces/mamba/docs/draft-phase1.md:24-30):
-      deltaA[c,s,m] = exp(delta[c,m] * a[c,s]); deltaBu[c,s,m] = delta[c,m]*b[s,m]*u[c,m]
-      state_m = deltaA_m * state_{m-1} + deltaBu_m (state_{-1} = 0)
-      out[c,m] = sum_s c[s,m] * state_m[c,s]
+    """Selective scan, sequential over M, in the operation order of the reference's
+    numpy forward (workspaces/mamba/docs/draft-phase1.md:24-30):
+      deltaA   = exp(delta[:, None, :] * a[:, :, None])           (C, S, M)
+      deltaB_u = delta[:, None, :] * b[None, :, :] * u[:, None, :] (C, S, M)
+      state_i  = deltaA[..., i] * state_{i-1} + deltaB_u[..., i]   (state_{-1} = 0)
+      out      = sum over axis 1 (S) of c[None] * scan_res          (C, M)
+    numpy reduces axis 1 of a C-ordered (C, S, M) array one S-row at a time
+    (s = 0, 1, ..., S-1), so the state sum is sequential in s.
     delta, u: (C, M); a: (C, S); b, c: (S, M) -> out (C, M), fp32."""
     delta, u, a, b, c = map(_f32, (delta, u, a, b, c))
     ch, m_len = delta.shape
     s_len = a.shape[1]
+    delta_a = np.exp(delta[:, None, :] * a[:, :, None]).astype(F32)
+    delta_bu = (delta[:, None, :] * b[None, :, :] * u[:, None, :]).astype(F32)
+    scan_res = np.empty((ch, s_len, m_len), dtype=F32)
     state = np.zeros((ch, s_len), dtype=F32)
-    out = np.empty((ch, m_len), dtype=F32)
-    for m in range(m_len):
-        dm = delta[:, m:m + 1]                                        # (C, 1)
-        d_a = np.exp(dm * a).astype(F32)                              # (C, S)
-        d_bu = ((dm * b[None, :, m]) * u[:, m:m + 1]).astype(F32)     # (C, S)
-        state = (d_a * state + d_bu).astype(F32)
-        out[:, m] = np.sum(state * c[None, :, m], axis=1)
-    return out
+    for i in range(m_len):
+        state = delta_a[..., i] * state + delta_bu[..., i]
+        scan_res[..., i] = state
+    return np.sum(c[None, :, :] * scan_res, axis=1).astype(F32)

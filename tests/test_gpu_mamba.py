@@ -1,13 +1,16 @@
-"""GPU parity: the Mamba selective scan vs the fp32 numpy oracle.
+"""GPU parity: the Mamba chunked scan vs the fp32 numpy oracle.
 
-The kernel rounds every step as the numpy definition does (numpy's float32 exp,
-no contraction, numpy's pairwise sum over the states), so the comparison is
-bit-exact; relative-L2 (the reference's gate is 3e-5 for this kernel,
-adapter/nkibench_case.py:53) is printed alongside.
+The oracle evaluates the reference forward sequentially; the kernel scans 8-step
+chunks in parallel (fp64 chunk products and scan), so its outputs differ in the
+last bits.  Gate: relative-L2 <= 1e-5 (the fp32 gate; the reference's own gate
+for this kernel is 3e-5, adapter/nkibench_case.py:53).  Where no chunk boundary
+is involved (M <= 8) the kernel rounds every step as the oracle does, so those
+cases and the device exp are compared bit for bit.
 
 Full NKIBench shape (C=256, M=7168, S=16) on the five seeds, shapes that put the
-block boundaries, a ragged last block and every state count in play, and a direct
-check of the device exp against np.exp."""
+chunk and segment boundaries, ragged tails, misaligned rows and every state
+count in play, strong decay, and a direct check of the device exp against
+np.exp."""
 import numpy as np
 import pytest
 import torch
@@ -29,32 +32,56 @@ def _run(d, label):
     return got, want
 
 
-def test_full_size_all_seeds_bit_exact():
-    for s in SEEDS:
-        got, want = _run(oi.draw("mamba", s), f"seed={s}")
-        np.testing.assert_array_equal(got, want)
+GATE = 1e-5
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_full_size_all_seeds(seed):
+    got, want = _run(oi.draw("mamba", seed), f"seed={seed}")
+    assert rel_l2(got, want) < GATE
+    assert np.isfinite(got).all()
 
 
 @pytest.mark.parametrize("dims", [
-    dict(C=4, M=192, S=16),       # exactly one block
-    dict(C=5, M=193, S=16),       # a one-step last block
-    dict(C=7, M=1000, S=5),       # ragged last block, S < 8
-    dict(C=3, M=31, S=1),         # single state, shorter than a 16-step group
-    dict(C=6, M=2049, S=12),      # 8 < S < 16: pairwise tree then sequential tail
-    dict(C=2, M=400, S=8),
+    dict(C=4, M=512, S=16),       # exactly one segment
+    dict(C=5, M=513, S=16),       # a one-step last segment
+    dict(C=7, M=1000, S=5),       # ragged last chunk and segment, S < 8
+    dict(C=3, M=31, S=1),         # single state, four chunks
+    dict(C=6, M=2049, S=12),
+    dict(C=2, M=4099, S=16),      # M % 4 != 0: scalar loads
+    dict(C=300, M=1536, S=3),     # more channels than compute units
 ])
-def test_small_and_ragged_bit_exact(dims):
+def test_small_and_ragged(dims):
     got, want = _run(oi.draw("mamba", 11, dims=dims), str(dims))
+    assert rel_l2(got, want) < GATE
+
+
+@pytest.mark.parametrize("dims", [dict(C=9, M=8, S=16), dict(C=3, M=5, S=7), dict(C=2, M=1, S=1)])
+def test_single_chunk_bit_exact(dims):
+    # one chunk: the entry state is exactly 0 and every step rounds as numpy does
+    got, want = _run(oi.draw("mamba", 5, dims=dims), str(dims))
     np.testing.assert_array_equal(got, want)
 
 
-def test_strong_decay_bit_exact():
-    # |delta*a| up to ~10: dA far from 1, exp over many binades
+def test_strong_decay():
+    # |delta*a| up to ~10: dA far from 1, exp over many binades (general exp path)
     d = oi.draw("mamba", 2, dims=dict(C=8, M=1536, S=16))
     d["delta"] = (np.abs(d["delta"]) * 40).astype(np.float32)
     d["a"] = (-np.abs(d["a"]) * 40).astype(np.float32)
     got, want = _run(d, "strong decay")
-    np.testing.assert_array_equal(got, want)
+    assert rel_l2(got, want) < GATE
+
+
+def test_misaligned_rows():
+    # inputs at a 4-byte offset: the kernel takes its scalar-load path
+    d = oi.draw("mamba", 3, dims=dict(C=4, M=700, S=16))
+    dev = {}
+    for k, v in d.items():
+        t = torch.zeros(v.size + 1, device="cuda")
+        t[1:] = torch.from_numpy(v.ravel()).cuda()
+        dev[k] = t[1:].view(v.shape)
+    got = to_host(ops.mamba(**dev))
+    assert rel_l2(got, oo.mamba(**d)) < GATE
 
 
 def test_device_exp_matches_numpy():

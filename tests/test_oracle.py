@@ -228,6 +228,32 @@ def test_mamba_closed_form_tiny():
     assert rel_l2(oo.mamba(**d), want) < 1e-6
 
 
+def test_mamba_state_sum_order():
+    """The oracle sums the 16 states in sequence (s = 0..15), as numpy reduces axis 1
+    of the reference's (C, S, M) array.  An explicit s-loop gives the same bits; a
+    pairwise sum over a contiguous S axis (numpy's order for axis=-1) agrees to ~1e-7
+    but not bit for bit, so a bit-exact comparison is only valid in one order."""
+    d = oi.draw("mamba", 42, dims=dict(C=16, M=512, S=16))
+    out = oo.mamba(**d)
+    delta, u, a, b, c = (d[k] for k in ("delta", "u", "a", "b", "c"))
+    F = np.float32
+    state = np.zeros((16, 16), dtype=F)
+    seq = np.empty((16, 512), dtype=F)
+    pair = np.empty((16, 512), dtype=F)
+    for i in range(512):
+        dm = delta[:, i:i + 1]
+        state = (np.exp(dm * a).astype(F) * state + (dm * b[None, :, i]) * u[:, i:i + 1]).astype(F)
+        prod = state * c[None, :, i]
+        acc = prod[:, 0].copy()
+        for s in range(1, 16):
+            acc = acc + prod[:, s]
+        seq[:, i] = acc
+        pair[:, i] = np.sum(prod, axis=1)          # contiguous axis: pairwise blocks
+    np.testing.assert_array_equal(out, seq)
+    assert (out != pair).sum() > 100
+    assert rel_l2(pair, out) < 1e-6
+
+
 def test_mamba_reference_known_answer_seed42():
     # workspaces/mamba/docs/draft-phase1.md:93-96: ||out|| ~ 2.055, max|out| ~ 0.0127
     out = oo.mamba(**oi.draw("mamba", 42))
