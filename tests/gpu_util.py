@@ -13,3 +13,24 @@ def to_dev(a, dev, dtype=torch.float32):
 
 def to_host(t):
     return t.detach().to(torch.float32).cpu().numpy()
+
+
+def elementwise_in_slices(fn, arrays, n_out=1, parts=16):
+    """fn(*arrays) for an elementwise fn, evaluated on `parts` contiguous slices in
+    threads (numpy releases the GIL in its loops) and concatenated: the same values
+    as one call, in a fraction of the time for 2^27-element buffers."""
+    from concurrent.futures import ThreadPoolExecutor
+    n = arrays[0].shape[0]
+    bounds = [(i * n // parts, (i + 1) * n // parts) for i in range(parts)]
+    with ThreadPoolExecutor(max_workers=8) as pool:
+        res = list(pool.map(lambda b: fn(*(a[b[0]:b[1]] for a in arrays)), bounds))
+    if n_out == 1:
+        return np.concatenate(res)
+    return tuple(np.concatenate([r[j] for r in res]) for j in range(n_out))
+
+
+def threaded_heads(fn, heads, workers=8):
+    """Stacks fn((b, h)) over heads, evaluated in a thread pool."""
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        return np.stack(list(pool.map(fn, heads)))
