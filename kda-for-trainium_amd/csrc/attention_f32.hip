@@ -2,7 +2,7 @@
 // fp16 MFMA, flash style: scores never leave the chip, fp32 online softmax.
 //
 //   out[b, h, s, :] = softmax_j(q[b, s, h, :] . k[b, j, h/G, :] * scale) @ v[b, j, h/G, :]
-//   (G = 2 query heads per kv head; causal: keys j > s masked; output strides free)
+//   (G = Hq / Hkv query heads per kv head; causal: keys j > s masked; output strides free)
 //
 // Precision.  The fp32 gate (relative L2 <= 1e-5) rules out bf16 operands.  Each
 // operand is scaled by a power of two and split into two fp16 limbs,
@@ -21,9 +21,11 @@
 // workspace; q is split by the attention kernel itself as it loads it (once per
 // wave; a q pre-pass cost 11 us of 373 at the NKIBench shape).
 //
-// Work decomposition: one workgroup = (batch b, kv head, block of 128 queries);
-// its 8 waves are the 2 query heads of that kv head x 4 quarters of the query
-// block (32 rows each), so each K/V tile staged in LDS serves 256 query rows.
+// Work decomposition: one workgroup = (batch b, kv head, HPW of its query heads,
+// block of 256 / HPW queries), HPW the largest power of two up to 8 dividing G;
+// its 8 waves are the HPW heads x 8 / HPW blocks of 32 query rows, so each K/V
+// tile staged in LDS serves 256 query rows (the NKIBench G = 2: 2 heads x 128
+// queries).
 // K and V tiles of 64 keys (both limbs, 32 KiB each) go global->LDS by DMA
 // through 2-slot rings and are read with the same fragment scheme as the bf16
 // kernel: K [key][d] with 16-byte chunk c of row r at c ^ kswz(r), rows read in
@@ -47,10 +49,7 @@ constexpr int kD = 128;                      // head dim
 constexpr int kBN = 64;                      // keys per tile
 constexpr int kWaveRows = 32;                // query rows per wave
 constexpr int kIT = kWaveRows / 16;
-constexpr int kGroup = 2;                    // query heads per kv head
-constexpr int kRowWaves = 4;                 // waves per query head
-constexpr int kBM = kWaveRows * kRowWaves;   // 128 query rows per workgroup and head
-constexpr int kWaves = kGroup * kRowWaves;   // 8
+constexpr int kWaves = 8;                    // HPW query heads x (8 / HPW) blocks of 32 rows
 constexpr int kThreads = 64 * kWaves;
 constexpr int kPlaneBytes = kBN * kD * 2;    // one limb of a K or V tile: 16 KiB
 constexpr int kTileBytes = 2 * kPlaneBytes;  // both limbs: 32 KiB
@@ -197,8 +196,12 @@ __device__ __forceinline__ uint32_t pack_h2(_Float16 lo, _Float16 hi) {
   return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
 }
 
-template <bool CAUSAL>
+// HPW query heads (of one kv head) per workgroup, HPW in {1, 2, 4, 8}: the
+// workgroup covers BM = 32 * 8 / HPW query rows of each of its heads, and a kv
+// head's G query heads are spread over G / HPW workgroups.
+template <bool CAUSAL, int HPW>
 __global__ __launch_bounds__(kThreads, 1) void gqa_f32_kernel(Args p) {
+  constexpr int kBM = kWaveRows * kWaves / HPW;
   __shared__ __align__(1024) uint8_t smem[4 * kTileBytes];   // K slots 0,1; V slots 2,3
 
   const int lane = threadIdx.x & 63;
@@ -207,14 +210,18 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_f32_kernel(Args p) {
   const int g = lane >> 4;
 
   const int nqb = (p.seq + kBM - 1) / kBM;
-  const int nbh = p.batch * p.hkv;
+  const int group = p.hq / p.hkv;
+  const int nsplit = group / HPW;                   // workgroups per kv head
+  const int nbh = p.batch * p.hkv * nsplit;
   // longest causal blocks first
   const int qb = CAUSAL ? (nqb - 1 - (int)blockIdx.x / nbh) : ((int)blockIdx.x / nbh);
   const int bh = blockIdx.x % nbh;
-  const int b = bh / p.hkv, kvh = bh % p.hkv;
-  const int h = kvh * kGroup + (wave % kGroup);
+  const int b = bh / (p.hkv * nsplit);
+  const int kvh = (bh / nsplit) % p.hkv;
+  const int h = kvh * group + (bh % nsplit) * HPW + (wave % HPW);
+  const int bkv = b * p.hkv + kvh;                  // index of the per-(b, kv head) scales
   const int q0 = qb * kBM;
-  const int w0 = q0 + (wave / kGroup) * kWaveRows;   // this wave's first query row
+  const int w0 = q0 + (wave / HPW) * kWaveRows;     // this wave's first query row
 
   // ---- Q fragments (MFMA B operand, two limbs): row w0 + 16it + l16, d = 32dc + 8g .. +7.
   // Each row is scaled by 2^(kTopExp - e), e the exponent of its largest |value|
@@ -297,7 +304,7 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_f32_kernel(Args p) {
   const int nkt = CAUSAL ? min(nkt_all, (q0 + kBM - 1) / kBN + 1) : nkt_all;
   int nfree = p.seq / kBN;                          // full tiles
   if (CAUSAL) nfree = min(nfree, (q0 + 1) / kBN);   // keys j0+63 <= q0 for every row
-  const float* kinv = p.kinv + (int64_t)bh * p.nt;
+  const float* kinv = p.kinv + (int64_t)bkv * p.nt;
 
   auto tile_step = [&](auto mask_tag, int kt) {
     constexpr bool MASK = decltype(mask_tag)::value;
@@ -427,7 +434,7 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_f32_kernel(Args p) {
   }
 
   // ---- normalise and store: lane holds out[row][d = 16dt + 4g .. +3]
-  const float vs = p.vinv[bh] / kPScale;
+  const float vs = p.vinv[bkv] / kPScale;
   float* op = p.out + b * p.o_sb + (int64_t)h * p.o_sh;
 #pragma unroll
   for (int it = 0; it < kIT; ++it) {
@@ -493,9 +500,9 @@ extern "C" int kda_gqa_fwd_f32(const float* q, const float* k, const float* v, f
   if (head_dim != kD)
     return set_error(KDA_ERR_UNSUPPORTED, "%s: head_dim %lld unsupported (only %d)", what,
                      (long long)head_dim, kD);
-  if (hq % hkv || hq / hkv != kGroup)
-    return set_error(KDA_ERR_UNSUPPORTED,
-                     "%s: needs Hq/Hkv == %d query heads per kv head (got %lld/%lld)", what, kGroup,
+  if (hq % hkv)
+    return set_error(KDA_ERR_INVALID_ARG,
+                     "%s: Hq=%lld is not a multiple of Hkv=%lld query heads per kv head", what,
                      (long long)hq, (long long)hkv);
   if (!(scale > 0.f)) return set_error(KDA_ERR_INVALID_ARG, "%s: scale must be > 0", what);
   if (batch == 0 || seq == 0) return KDA_OK;
@@ -505,7 +512,11 @@ extern "C" int kda_gqa_fwd_f32(const float* q, const float* k, const float* v, f
   if ((out_stride_s % 4) || (out_stride_h % 4) || (out_stride_b % 4))
     return set_error(KDA_ERR_INVALID_ARG, "%s: output strides must be multiples of 4", what);
   const int64_t nt = (seq + kBN - 1) / kBN;
-  const int64_t nblocks = ((seq + kBM - 1) / kBM) * batch * hkv;
+  // heads per workgroup: the largest power of two up to 8 that divides the group
+  const int64_t group = hq / hkv;
+  const int hpw = (group % 8 == 0) ? 8 : (group % 4 == 0) ? 4 : (group % 2 == 0) ? 2 : 1;
+  const int64_t bm = kWaveRows * kWaves / hpw;
+  const int64_t nblocks = ((seq + bm - 1) / bm) * batch * hkv * (group / hpw);
   if (nblocks > 0x7fffffff || seq > (1 << 24) || batch * hkv > 65535 || nt > 0x7fffffff ||
       batch * seq * hq * kD * 2 > ((int64_t)1 << 32))
     return set_error(KDA_ERR_UNSUPPORTED, "%s: problem too large", what);
@@ -540,9 +551,18 @@ extern "C" int kda_gqa_fwd_f32(const float* q, const float* k, const float* v, f
   a.hkv = (int)hkv;
   a.nt = (int)nt;
   a.scale_log2 = scale * 1.4426950408889634f;
-  if (causal)
-    hipLaunchKernelGGL(gqa_f32_kernel<true>, dim3((unsigned)nblocks), dim3(kThreads), 0, st, a);
-  else
-    hipLaunchKernelGGL(gqa_f32_kernel<false>, dim3((unsigned)nblocks), dim3(kThreads), 0, st, a);
+  const dim3 grid((unsigned)nblocks), block(kThreads);
+#define KDA_GQA_LAUNCH(H)                                                         \
+  if (causal)                                                                     \
+    hipLaunchKernelGGL((gqa_f32_kernel<true, H>), grid, block, 0, st, a);         \
+  else                                                                            \
+    hipLaunchKernelGGL((gqa_f32_kernel<false, H>), grid, block, 0, st, a);
+  switch (hpw) {
+    case 8: KDA_GQA_LAUNCH(8) break;
+    case 4: KDA_GQA_LAUNCH(4) break;
+    case 2: KDA_GQA_LAUNCH(2) break;
+    default: KDA_GQA_LAUNCH(1) break;
+  }
+#undef KDA_GQA_LAUNCH
   return check_launch(what);
 }

@@ -13,7 +13,9 @@ Each operator directory ``<root>/<op>/`` holds
 ``summarize`` follows scripts/summary.py:29-95,137-141: a record counts only if
 it passed the full five-seed gate with a numeric speedup and its verdict is not
 a rejection, a drop or a fast screen; per operator the best such speedup is
-reported, and the aggregate is their geometric mean.
+reported, and the aggregate is their geometric mean.  Beside it, the latest
+passing record of each operator (bench.py rows are checked on one seed) and the
+geomean of those are reported.
 
     python -m kda.ledger <root> [--json]
 """
@@ -100,8 +102,10 @@ def is_validated(d: Dict[str, Any]) -> bool:
 
 
 def scan_op(root: os.PathLike, op: str) -> Dict[str, Any]:
-    """Best validated speedup of one operator and the count of validated records."""
+    """Best validated speedup of one operator, the count of validated records, and
+    the latest passing record of any kind (e.g. a bench row checked on one seed)."""
     best = None
+    latest = None
     n_pass = n_all = 0
     path = Path(root) / op / "candidates.jsonl"
     if path.exists():
@@ -114,6 +118,8 @@ def scan_op(root: os.PathLike, op: str) -> Dict[str, Any]:
             except json.JSONDecodeError:
                 continue
             n_all += 1
+            if d.get("passed") and isinstance(d.get("speedup"), (int, float)):
+                latest = d
             if is_validated(d):
                 n_pass += 1
                 if best is None or d["speedup"] > best["speedup"]:
@@ -121,7 +127,11 @@ def scan_op(root: os.PathLike, op: str) -> Dict[str, Any]:
     return {"op": op, "best_speedup": best["speedup"] if best else None,
             "best_candidate": best["candidate"] if best else None,
             "best_latency_ms": best["latency_ms"] if best else None,
-            "n_validated": n_pass, "n_records": n_all}
+            "n_validated": n_pass, "n_records": n_all,
+            "latest_speedup": latest["speedup"] if latest else None,
+            "latest_latency_ms": latest["latency_ms"] if latest else None,
+            "latest_seeds": latest["seeds"] if latest else None,
+            "latest_verdict": latest.get("verdict") if latest else None}
 
 
 def summarize(root: os.PathLike) -> Dict[str, Any]:
@@ -130,9 +140,12 @@ def summarize(root: os.PathLike) -> Dict[str, Any]:
     rows = [scan_op(root, op) for op in ops]
     speeds = [r["best_speedup"] for r in rows if r["best_speedup"]]
     geo = math.exp(sum(math.log(s) for s in speeds) / len(speeds)) if speeds else None
+    lat = [r["latest_speedup"] for r in rows if r["latest_speedup"]]
+    geo_latest = math.exp(sum(math.log(s) for s in lat) / len(lat)) if lat else None
     return {"ops": rows, "n_with_validated": len(speeds), "n_ops": len(rows),
             "geomean_best_speedup": geo,
-            "range": [min(speeds), max(speeds)] if speeds else None}
+            "range": [min(speeds), max(speeds)] if speeds else None,
+            "n_with_latest": len(lat), "geomean_latest_speedup": geo_latest}
 
 
 def main(argv: Optional[List[str]] = None) -> int:
@@ -144,14 +157,21 @@ def main(argv: Optional[List[str]] = None) -> int:
     if args.json:
         print(json.dumps(s, indent=2))
         return 0
-    rows = sorted(s["ops"], key=lambda r: r["best_speedup"] or -1, reverse=True)
-    print(f"{'op':26s} {'best':>12s} {'p50 ms':>10s}  validated/records")
-    print("-" * 70)
+    rows = sorted(s["ops"], key=lambda r: r["best_speedup"] or r["latest_speedup"] or -1, reverse=True)
+    print(f"{'op':26s} {'best (5 seeds)':>15s} {'p50 ms':>10s}  {'latest':>12s} {'p50 ms':>10s}  "
+          f"validated/records")
+    print("-" * 96)
     for r in rows:
         bs = f"{r['best_speedup']:.3f}x" if r["best_speedup"] else "-"
         lat = f"{r['best_latency_ms']:.4f}" if r["best_latency_ms"] is not None else "-"
-        print(f"{r['op']:26s} {bs:>12s} {lat:>10s}  {r['n_validated']}/{r['n_records']}")
-    print("-" * 70)
+        ls = f"{r['latest_speedup']:.3f}x" if r["latest_speedup"] else "-"
+        llat = f"{r['latest_latency_ms']:.4f}" if r["latest_latency_ms"] is not None else "-"
+        print(f"{r['op']:26s} {bs:>15s} {lat:>10s}  {ls:>12s} {llat:>10s}  "
+              f"{r['n_validated']}/{r['n_records']}")
+    print("-" * 96)
+    if s["geomean_latest_speedup"]:
+        print(f"geomean(latest passing)     : {s['geomean_latest_speedup']:.3f}x over "
+              f"{s['n_with_latest']} ops (latest rows may be single-seed bench checks)")
     if s["geomean_best_speedup"]:
         lo, hi = s["range"]
         print(f"ops with a validated result : {s['n_with_validated']}/{s['n_ops']}")

@@ -454,10 +454,10 @@ def gqa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = False,
     """Grouped-query softmax attention: per query head h (kv head h // (Hq/Hkv)),
     ``softmax(q k^T * scale) v`` with an fp32 online softmax (flash style).
 
-    bf16 q/k/v (4 query heads per kv head) run on bf16 MFMA and return bf16; fp32
-    q/k/v (2 query heads per kv head, the reference's gqa_full case) run on a
-    two-limb fp16 split with fp32-class accuracy and return fp32 (workspace:
-    KDA_OP_GQA_F32 bytes, allocated when not given).
+    bf16 q/k/v run on bf16 MFMA and return bf16; fp32 q/k/v (the reference's
+    gqa_full case) run on a two-limb fp16 split with fp32-class accuracy and
+    return fp32 (workspace: KDA_OP_GQA_F32 bytes, allocated when not given).
+    Any Hq that is a multiple of Hkv; head dim 128.
 
     q (B, S, Hq, D), k/v (B, S, Hkv, D); scale defaults to 1/sqrt(D); causal masks
     keys after the query.  out_layout "bshd" returns (B, S, Hq, D); "bhsd" returns

@@ -83,6 +83,18 @@ def test_gqa_rejects_unsupported(dev):
     with pytest.raises(ValueError, match="head_dim"):
         ops.gqa(q, kv, kv)
     q = torch.zeros(1, 8, 6, 128, device=dev, dtype=BF)
-    kv = torch.zeros(1, 8, 3, 128, device=dev, dtype=BF)
-    with pytest.raises(ValueError, match="query heads per kv head"):
+    kv = torch.zeros(1, 8, 4, 128, device=dev, dtype=BF)
+    with pytest.raises(ValueError, match="not a multiple"):
         ops.gqa(q, kv, kv)
+
+
+# Every group size: a workgroup serves the largest power of two up to 8 that
+# divides G of a kv head's query heads (G = 3, 6: 1 and 2 heads per workgroup).
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("hq,hkv", [(2, 2), (4, 2), (6, 2), (6, 1), (16, 2), (16, 1), (12, 3)])
+def test_gqa_group_sizes(dev, causal, hq, hkv):
+    d = oi.draw("gqa_cfg", hq * 10 + hkv, dims=dict(B=2, S=300, HQ=hq, HKV=hkv, D=128))
+    out = to_host(ops.gqa(*(to_dev(d[k], dev, BF) for k in ("q", "k", "v")), causal=causal))
+    err = rel_l2(out, oo.gqa(d["q"], d["k"], d["v"], causal=causal))
+    print(f"gqa bf16 Hq={hq} Hkv={hkv} causal={causal} rel_l2={err:.3e}", flush=True)
+    assert err < 5e-3

@@ -89,10 +89,29 @@ def test_gqa_f32_causal_first_row_is_v0(dev):
 
 
 def test_gqa_f32_rejects_unsupported(dev):
-    q = torch.zeros(1, 8, 4, 128, device=dev)
-    kv = torch.zeros(1, 8, 1, 128, device=dev)
-    with pytest.raises(ValueError, match="query heads per kv head"):
+    q = torch.zeros(1, 8, 6, 128, device=dev)
+    kv = torch.zeros(1, 8, 4, 128, device=dev)
+    with pytest.raises(ValueError, match="not a multiple"):
         ops.gqa(q, kv, kv)
     with pytest.raises(ValueError, match="head_dim"):
         ops.gqa(torch.zeros(1, 8, 2, 64, device=dev), torch.zeros(1, 8, 1, 64, device=dev),
                 torch.zeros(1, 8, 1, 64, device=dev))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("hq,hkv", [(1, 1), (4, 1), (8, 1), (6, 2), (16, 2)])
+def test_gqa_f32_group_sizes(dev, causal, hq, hkv):
+    d = oi.draw("gqa_full", hq * 10 + hkv, dims=dict(B=1, S=200, HQ=hq, HKV=hkv, D=128))
+    out = to_host(ops.gqa(*_qkv(d, dev), causal=causal))
+    err = rel_l2(out, oo.gqa(d["q"], d["k"], d["v"], causal=causal))
+    print(f"gqa f32 Hq={hq} Hkv={hkv} causal={causal} rel_l2={err:.3e}", flush=True)
+    assert err < GATE
+
+
+def test_gqa_full_kwargs_contract(dev):
+    """ops.gqa_full(**{q, k, v}) is the NKIBench forward: non-causal, (B, Hq, S, D)."""
+    d = oi.draw("gqa_full", 4, dims=dict(B=1, S=256, HQ=4, HKV=2, D=128))
+    out = ops.gqa_full(**{k: to_dev(v, dev) for k, v in d.items()})
+    assert tuple(out.shape) == (1, 4, 256, 128)
+    want = oo.gqa(d["q"], d["k"], d["v"], causal=False, out_layout="bhsd")
+    assert rel_l2(to_host(out), want) < GATE
