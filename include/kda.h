@@ -117,6 +117,23 @@ int kda_rmsnorm_matmul_bf16(const kda_bf16* x, const kda_bf16* gamma, const kda_
                             kda_bf16* y, int64_t m, int64_t k, int64_t n, float eps,
                             void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Bytes of the per-device static buffer behind kda_rmsnorm_matmul_bf16_noalloc. */
+#define KDA_NOALLOC_SCRATCH_BYTES (64LL << 20)
+
+/* kda_rmsnorm_matmul_bf16 without a workspace argument and without any allocation:
+ * no counterpart in the reference; for callers that cannot allocate (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  The
+ * workspace is a file-scope device buffer of KDA_NOALLOC_SCRATCH_BYTES that every
+ * device the library runs on holds until the process ends; its address is looked
+ * up once per device (no allocation).  Sizes whose workspace (2*M*K + 4*M bytes)
+ * exceeds it are rejected with KDA_ERR_UNSUPPORTED before any launch.  All calls
+ * on one device share the buffer: calls that overlap on one device (different
+ * streams, or host threads without ordering) race and must not be issued.
+ * Results equal kda_rmsnorm_matmul_bf16's bit for bit. */
+int kda_rmsnorm_matmul_bf16_noalloc(const kda_bf16* x, const kda_bf16* gamma, const kda_bf16* w,
+                                    kda_bf16* y, int64_t m, int64_t k, int64_t n, float eps,
+                                    void* stream);
+
 /* y[M,K] = (silu(x @ w_gate) * (x @ w_up)) @ w_down with x [M,K], w_up/w_gate [K,F],
  * w_down [F,K].  h is caller-provided scratch of M*F bf16 (the gated activation,
  * written by the first kernel and read by the second).  `workspace` (optional:

@@ -44,6 +44,8 @@
 // tile ids are remapped onto one XCD (sharing its L2), then walked in groups of
 // kGroupM tile-rows so co-resident tiles reuse the same A rows and B columns.
 #include <math.h>
+
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1149,6 +1151,56 @@ extern "C" int kda_rmsnorm_matmul_bf16(const kda_bf16* x, const kda_bf16* gamma,
   p.row_scale = wp.inv;
   add_seg(p, wp.xg, k, w, n, k);
   return launch_auto<true, Epi::kRowScale>(p, 1, st, what);
+}
+
+// ---- allocation-free RMSNorm -> matmul -------------------------------------
+// A file-scope device buffer stands in for the caller's workspace.  Its name is
+// not a device address in host code: the address is resolved once per device with
+// hipGetSymbolAddress (the device current at the first call) and cached; only that
+// address is ever passed to a kernel.  The prep kernel rewrites every byte of the
+// workspace it uses (normalised rows and 1/rms) before the GEMM reads them, so no
+// clearing is needed; each device keeps its buffer until the process ends.
+namespace {
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[KDA_NOALLOC_SCRATCH_BYTES];
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+int scratch_address(const char* what, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(KDA_ERR_HIP, "%s: no usable current device (%d)", what, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(KDA_ERR_HIP, "%s: hipGetSymbolAddress of the scratch buffer failed: %s",
+                       what, hipGetErrorString(e));
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return KDA_OK;
+}
+}  // namespace
+
+extern "C" int kda_rmsnorm_matmul_bf16_noalloc(const kda_bf16* x, const kda_bf16* gamma,
+                                               const kda_bf16* w, kda_bf16* y, int64_t m,
+                                               int64_t k, int64_t n, float eps, void* stream) {
+  clear_error();
+  const char* what = "rmsnorm_matmul_bf16_noalloc";
+  const int64_t need = workspace_bytes(KDA_OP_RMSNORM_MATMUL_BF16, 1, m, k, n, 0);
+  if (need > KDA_NOALLOC_SCRATCH_BYTES)
+    return set_error(KDA_ERR_UNSUPPORTED,
+                     "%s: M=%lld K=%lld needs %lld bytes of scratch; the static buffer holds %lld "
+                     "(2*M*K + 4*M bytes must fit)",
+                     what, (long long)m, (long long)k, (long long)need,
+                     (long long)KDA_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need > 0)   // negative sizes are reported by the call below, before any launch
+    if (int rc = scratch_address(what, &ws)) return rc;
+  return kda_rmsnorm_matmul_bf16(x, gamma, w, y, m, k, n, eps, ws, KDA_NOALLOC_SCRATCH_BYTES,
+                                 stream);
 }
 
 extern "C" int kda_swiglu_bf16(const kda_bf16* x, const kda_bf16* w_up, const kda_bf16* w_down,

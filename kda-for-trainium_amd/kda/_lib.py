@@ -30,6 +30,7 @@ SIGNATURES = {
     "kda_rope_f32": [_p, _p, _p, _p, _i64, _i64, _p],
     "kda_matmul_bf16": [_p, _p, _p, _i64, _i64, _i64, _p],
     "kda_rmsnorm_matmul_bf16": [_p, _p, _p, _p, _i64, _i64, _i64, _f32, _p, _i64, _p],
+    "kda_rmsnorm_matmul_bf16_noalloc": [_p, _p, _p, _p, _i64, _i64, _i64, _f32, _p],
     "kda_workspace_size": [_int, _i64, _i64, _i64, _i64, _i64],
     "kda_matmul_f32": [_p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
     "kda_transpose_matmul_f32": [_p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
