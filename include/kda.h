@@ -94,7 +94,10 @@ enum {
 };
 
 /* Workspace bytes for operator `op` at the given sizes (unused sizes: 0);
- * -1 for an unknown op or a negative size. */
+ * -1 for an unknown op or a negative size.  The sizes do not depend on the
+ * device, except KDA_OP_SWIGLU_BF16 (an optional workspace whose split-K tail is
+ * planned for the current device's compute-unit count: query it with the device
+ * current that will run the call; one that is too small only disables the split). */
 int64_t kda_workspace_size(int op, int64_t batch, int64_t m, int64_t k, int64_t n, int64_t r);
 
 /* ---------------------------------------------------------------- bf16 GEMMs

@@ -35,9 +35,11 @@ int64_t gqa_f32_workspace_bytes(int64_t batch, int64_t seq, int64_t hq, int64_t 
 
 // ---- device helpers -------------------------------------------------------
 
-// fp32 -> bf16 bits, round to nearest even (finite inputs; NaN stays NaN).
+// fp32 -> bf16 bits, round to nearest even; a NaN stays a NaN (sign kept, quiet
+// bit set: adding the rounding bias to a NaN could carry it into +0 or infinity).
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
   u += 0x7fffu + ((u >> 16) & 1u);
   return u >> 16;
 }

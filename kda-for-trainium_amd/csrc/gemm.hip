@@ -976,12 +976,17 @@ SplitPlan plan_split(Carve& c, int64_t count_a, int64_t count_b) {
   return s;
 }
 // K-chunks for the small GEMM t = x @ a [M, R]: its 256x128 tiles would occupy few
-// CUs (4096 x 128: 16 tiles), so K is split into up to 16 chunks run as a batch
-// into fp32 partials (each chunk a whole number of 64-deep k-tiles).
+// CUs (4096 x 128: 16 tiles), so K is split into up to kLoraMaxParts chunks run as
+// a batch into fp32 partials (each chunk a whole number of 64-deep k-tiles).  The
+// count depends on the device's CU count; the workspace always holds
+// kLoraMaxParts partials, so its size does not.
+constexpr int kLoraMaxParts = 16;
 int lora_t_parts(int64_t m, int64_t k, int64_t r) {
   const int64_t tiles = ((m + 255) / 256) * ((r + 127) / 128);
   int parts = 1;
-  while (parts < 16 && tiles * parts * 2 <= device_cu_count() && k % (parts * 2 * 64) == 0) parts *= 2;
+  while (parts < kLoraMaxParts && tiles * parts * 2 <= device_cu_count() &&
+         k % (parts * 2 * 64) == 0)
+    parts *= 2;
   return parts;
 }
 struct LoraPlan {
@@ -998,7 +1003,7 @@ LoraPlan plan_lora(Carve& c, int64_t m, int64_t k, int64_t n, int64_t r) {
   p.ah = c.take<uint16_t>(k * r);
   p.al = c.take<uint16_t>(k * r);
   p.parts = r > 0 ? lora_t_parts(m, k, r) : 1;
-  p.t = c.take<float>(p.parts * m * r);
+  p.t = c.take<float>(kLoraMaxParts * m * r);
   p.th = c.take<uint16_t>(m * r);
   p.tl = c.take<uint16_t>(m * r);
   p.bh = c.take<uint16_t>(r * n);

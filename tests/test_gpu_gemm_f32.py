@@ -129,3 +129,31 @@ def test_fp32_path_rejects_unaligned_k():
     w = torch.zeros(40, 64, device="cuda")
     with pytest.raises(ValueError, match="multiple of 32"):
         ops.matmul(x, w)
+
+
+@pytest.mark.parametrize("bits", [0xFFFFFFFF, 0x7F800001, 0xFFC00000])
+@pytest.mark.parametrize("op", ["matmul", "bmm"])
+def test_nan_inputs_propagate_through_the_split(op, bits):
+    """A NaN in lhs (any payload, either sign) splits into NaN limbs: exactly the
+    output rows it feeds are NaN, the others equal the NaN-free result."""
+    rng = np.random.default_rng(bits & 0xFFFF)
+    if op == "matmul":
+        lhs = rng.normal(size=(96, 64)).astype(np.float32)
+        rhs = rng.normal(size=(64, 72)).astype(np.float32)
+        bad = (5, 17)
+        fn = ops.matmul
+    else:
+        lhs = rng.normal(size=(2, 96, 64)).astype(np.float32)
+        rhs = rng.normal(size=(2, 64, 64)).astype(np.float32)
+        bad = (1, 5, 17)
+        fn = ops.bmm
+    clean = to_host(fn(to_dev(lhs, "cuda"), to_dev(rhs, "cuda")))
+    lhs_nan = lhs.copy()
+    lhs_nan.view(np.uint32)[bad] = np.uint32(bits)
+    assert np.isnan(lhs_nan[bad])
+    got = to_host(fn(to_dev(lhs_nan, "cuda"), to_dev(rhs, "cuda")))
+    row = bad[:-1]
+    assert np.isnan(got[row]).all()
+    mask = np.ones(got.shape[:-1], dtype=bool)
+    mask[row] = False
+    np.testing.assert_array_equal(got[mask], clean[mask])
