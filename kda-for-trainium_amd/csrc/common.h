@@ -35,22 +35,31 @@ int64_t gqa_f32_workspace_bytes(int64_t batch, int64_t seq, int64_t hq, int64_t 
 
 // ---- device helpers -------------------------------------------------------
 
-// fp32 -> bf16 bits, round to nearest even; a NaN stays a NaN (sign kept, quiet
-// bit set: adding the rounding bias to a NaN could carry it into +0 or infinity).
+// fp32 -> bf16 bits with gfx950's conversion instruction (v_cvt_pk_bf16_f32):
+// round to nearest even, fp32 denormals kept (bf16 shares fp32's exponent
+// range), overflow to infinity, and a NaN stays a NaN (quieted, sign kept).
+typedef float kda_floatx2 __attribute__((ext_vector_type(2)));
+typedef __bf16 kda_bf16x2 __attribute__((ext_vector_type(2)));
+
+// Packs two floats into one dword of two bf16 (lo in bits 0..15).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((kda_floatx2{lo, hi}), kda_bf16x2));
+}
+
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return pack_bf16x2(f, 0.0f) & 0xffffu;
 }
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
   return __builtin_bit_cast(float, b << 16);
 }
 
-// Packs two floats into one dword of two bf16 (lo in bits 0..15).
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+// Splits two floats into their bf16 (hi, lo) limbs, hi = bf16(x) and
+// lo = bf16(x - hi), packed in pairs (a in bits 0..15).
+__device__ __forceinline__ void split_bf16x2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  hi = pack_bf16x2(a, b);
+  lo = pack_bf16x2(a - __builtin_bit_cast(float, hi << 16),
+                   b - __builtin_bit_cast(float, hi & 0xffff0000u));
 }
 
 }  // namespace kda

@@ -464,10 +464,11 @@ __device__ __forceinline__ void split8(const float (&x)[8], bf16x8& hi, bf16x8& 
   u32x4 h, l;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
+    // one conversion per element keeps this kernel's register count lowest
     const uint32_t h0 = f32_to_bf16_bits(x[2 * e]), h1 = f32_to_bf16_bits(x[2 * e + 1]);
     const float r0 = x[2 * e] - bf16_bits_to_f32(h0), r1 = x[2 * e + 1] - bf16_bits_to_f32(h1);
     h[e] = h0 | (h1 << 16);
-    l[e] = f32_to_bf16_bits(r0) | (f32_to_bf16_bits(r1) << 16);
+    l[e] = pack_bf16x2(r0, r1);
   }
   hi = __builtin_bit_cast(bf16x8, h);
   lo = __builtin_bit_cast(bf16x8, l);
@@ -553,16 +554,11 @@ __global__ __launch_bounds__(256) void split_f32_kernel(const floatx4* __restric
                                                         int64_t n4) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
     const floatx4 v = __builtin_nontemporal_load(x + i);
-    uint32_t h[4];
-    float l[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      h[e] = f32_to_bf16_bits(v[e]);
-      l[e] = v[e] - bf16_bits_to_f32(h[e]);
-    }
-    hi[i] = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-    lo[i] = u32x2{f32_to_bf16_bits(l[0]) | (f32_to_bf16_bits(l[1]) << 16),
-                  f32_to_bf16_bits(l[2]) | (f32_to_bf16_bits(l[3]) << 16)};
+    uint32_t h0, h1, l0, l1;
+    split_bf16x2(v[0], v[1], h0, l0);
+    split_bf16x2(v[2], v[3], h1, l1);
+    hi[i] = u32x2{h0, h1};
+    lo[i] = u32x2{l0, l1};
   }
 }
 
@@ -574,16 +570,11 @@ __global__ __launch_bounds__(256) void sum_split_f32_kernel(const floatx4* __res
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
     floatx4 v = __builtin_nontemporal_load(part + i);
     for (int z = 1; z < parts; ++z) v += __builtin_nontemporal_load(part + z * n4 + i);
-    uint32_t h[4];
-    float l[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      h[e] = f32_to_bf16_bits(v[e]);
-      l[e] = v[e] - bf16_bits_to_f32(h[e]);
-    }
-    hi[i] = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-    lo[i] = u32x2{f32_to_bf16_bits(l[0]) | (f32_to_bf16_bits(l[1]) << 16),
-                  f32_to_bf16_bits(l[2]) | (f32_to_bf16_bits(l[3]) << 16)};
+    uint32_t h0, h1, l0, l1;
+    split_bf16x2(v[0], v[1], h0, l0);
+    split_bf16x2(v[2], v[3], h1, l1);
+    hi[i] = u32x2{h0, h1};
+    lo[i] = u32x2{l0, l1};
   }
 }
 
@@ -609,17 +600,16 @@ __global__ __launch_bounds__(256) void split_transpose_f32_kernel(const float* _
     const int mr = i / 8, kc = i % 8;    // mr: m within the block, kc: 8-element chunk of k
     const int64_t mm = m0 + mr, kk = k0 + 8 * kc;
     if (mm >= m || kk >= k) continue;
-    uint32_t h[8], l[8];
+    u32x4 h, l;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float v = tile[8 * kc + e][mr];
-      h[e] = f32_to_bf16_bits(v);
-      l[e] = f32_to_bf16_bits(v - bf16_bits_to_f32(h[e]));
+    for (int e = 0; e < 4; ++e) {
+      uint32_t he, le;
+      split_bf16x2(tile[8 * kc + 2 * e][mr], tile[8 * kc + 2 * e + 1][mr], he, le);
+      h[e] = he;
+      l[e] = le;
     }
-    *reinterpret_cast<u32x4*>(hi + mm * k + kk) =
-        u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
-    *reinterpret_cast<u32x4*>(lo + mm * k + kk) =
-        u32x4{l[0] | (l[1] << 16), l[2] | (l[3] << 16), l[4] | (l[5] << 16), l[6] | (l[7] << 16)};
+    *reinterpret_cast<u32x4*>(hi + mm * k + kk) = h;
+    *reinterpret_cast<u32x4*>(lo + mm * k + kk) = l;
   }
 }
 
@@ -693,18 +683,15 @@ __global__ __launch_bounds__(kRowThreads) void rms_split_f32_kernel(
   for (int c = tid; c < k4; c += kRowThreads) {
     floatx4 v = xr[c];
     if (zr) v += zr[c];
-    uint32_t h[4];
-    float l[4];
     const floatx4 gg = g ? gr[c] : floatx4{1.f, 1.f, 1.f, 1.f};
+    float y[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float y = (v[e] / rms) * gg[e];
-      h[e] = f32_to_bf16_bits(y);
-      l[e] = y - bf16_bits_to_f32(h[e]);
-    }
-    hr[c] = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-    lr[c] = u32x2{f32_to_bf16_bits(l[0]) | (f32_to_bf16_bits(l[1]) << 16),
-                  f32_to_bf16_bits(l[2]) | (f32_to_bf16_bits(l[3]) << 16)};
+    for (int e = 0; e < 4; ++e) y[e] = (v[e] / rms) * gg[e];
+    uint32_t h0, h1, l0, l1;
+    split_bf16x2(y[0], y[1], h0, l0);
+    split_bf16x2(y[2], y[3], h1, l1);
+    hr[c] = u32x2{h0, h1};
+    lr[c] = u32x2{l0, l1};
   }
 }
 

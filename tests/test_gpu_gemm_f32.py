@@ -114,6 +114,33 @@ def test_matmul_f32_layout_identity():
     assert rel_l2(got, b) < 1e-5
 
 
+def test_split_rounding_matches_rne_on_crafted_values():
+    """The device's bf16 conversion (hi = bf16(x), lo = bf16(x - hi)) equals
+    round-to-nearest-even on values built to hit its edge cases: exact ties of the
+    hi rounding with even and odd last bits, one below and above a tie, ties of
+    the residual, carries into the exponent, both signs, magnitudes 2^-100..2^100.
+    A = I makes the output exactly hi(B) + lo(B)."""
+    rng = np.random.default_rng(5)
+    k, n = 256, 264
+    top = rng.integers(0, 1 << 16, size=(k, n), dtype=np.uint32)
+    exp = rng.integers(127 - 100, 127 + 100, size=(k, n), dtype=np.uint32)
+    top = (top & np.uint32(0x807F)) | (exp << np.uint32(7))          # sign, exponent, 7 mantissa bits
+    low_patterns = np.array([0x8000, 0x7FFF, 0x8001, 0x0000, 0xFFFF, 0x4080, 0x2040, 0x1020,
+                             0x0180, 0xC080, 0x80C0, 0x3F80], dtype=np.uint32)
+    low = np.where(rng.random((k, n)) < 0.75,
+                   low_patterns[rng.integers(0, len(low_patterns), size=(k, n))],
+                   rng.integers(0, 1 << 16, size=(k, n), dtype=np.uint32))
+    bits = (top << np.uint32(16)) | low
+    bits[0, :8] = [0x3F808000, 0x3F818000, 0xBF808000, 0xBF818000,    # ties, even / odd hi
+                   0x7F7E8000, 0x7F7EFFFF, 0x0D800000, 0x0D808000]    # near bf16 max, tiny
+    b = bits.view(np.float32)
+    assert np.isfinite(b).all()
+    hi, lo = split_bf16x2(b)
+    assert np.isfinite(hi + lo).all()
+    got = to_host(ops.matmul(to_dev(np.eye(k, dtype=np.float32), "cuda"), to_dev(b, "cuda")))
+    np.testing.assert_array_equal(got.view(np.uint32), (hi + lo).view(np.uint32))
+
+
 def test_lora_rank_zero_term_matches_matmul():
     # b = 0 removes the low-rank term: lora == matmul
     d = oi.draw("lora", 3, dims=dict(M=256, K=128, N=256, R=32))
