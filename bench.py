@@ -126,7 +126,8 @@ NKIBENCH = {
     "mamba": dict(desc="delta,u[256,7168] a[256,16] b,c[16,7168]", dims=dict(C=256, M=7168, S=16),
                   bound="hbm",
                   work=4 * (3 * 256 * 7168 + 256 * 16 + 2 * 16 * 7168),
-                  note="sequential over 7168 steps per (channel, state): latency-bound"),
+                  note="chunked parallel scan; VALU-bound (numpy's float32 exp evaluated "
+                       "per (channel, state, step)), not HBM-bound"),
     "matmul": dict(desc="[4096,5120]@[5120,12288]", dims=dict(M=4096, K=5120, N=12288), bound="mfma", useful=_mm(4096, 5120, 12288),
                    work=3 * _mm(4096, 5120, 12288)),
     "transpose_matmul": dict(desc="[2048,4096]^T@[2048,10944]", dims=dict(M=4096, K=2048, N=10944),
