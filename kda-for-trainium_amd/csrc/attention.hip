@@ -155,23 +155,29 @@ __device__ __forceinline__ bool softmax_stats(State& st, const Args& p, int kt, 
           if (32 * (t >> 1) + 4 * (t & 1) + r > lim) s[it][t][r] = -INFINITY;
     }
   }
-  float m[kIT];
+  // Lane-partial maxima (16 values of each row per lane, a tree of three-input
+  // maxima).  A row's max exceeds its threshold iff one of its four lanes'
+  // partial maxima does (the threshold is the same in the four lanes), so the
+  // common case needs no cross-lane reduction: one compare per row and a ballot.
+  float x[kIT];
   bool grow_any = false;
 #pragma unroll
   for (int it = 0; it < kIT; ++it) {
-    // 16 values: seven three-input maxima and one two-input maximum
-    float x = __builtin_fmaxf(__builtin_fmaxf(s[it][0][0], s[it][0][1]), s[it][0][2]);
-    x = __builtin_fmaxf(__builtin_fmaxf(x, s[it][0][3]), s[it][1][0]);
-    x = __builtin_fmaxf(__builtin_fmaxf(x, s[it][1][1]), s[it][1][2]);
-    x = __builtin_fmaxf(__builtin_fmaxf(x, s[it][1][3]), s[it][2][0]);
-    x = __builtin_fmaxf(__builtin_fmaxf(x, s[it][2][1]), s[it][2][2]);
-    x = __builtin_fmaxf(__builtin_fmaxf(x, s[it][2][3]), s[it][3][0]);
-    x = __builtin_fmaxf(__builtin_fmaxf(x, s[it][3][1]), s[it][3][2]);
-    x = __builtin_fmaxf(x, s[it][3][3]);
-    m[it] = row_max4(x);
-    grow_any |= m[it] > st.m_grow[it];
+    const floatx4(&r)[4] = s[it];
+    const float a0 = __builtin_fmaxf(__builtin_fmaxf(r[0][0], r[0][1]), r[0][2]);
+    const float a1 = __builtin_fmaxf(__builtin_fmaxf(r[0][3], r[1][0]), r[1][1]);
+    const float a2 = __builtin_fmaxf(__builtin_fmaxf(r[1][2], r[1][3]), r[2][0]);
+    const float a3 = __builtin_fmaxf(__builtin_fmaxf(r[2][1], r[2][2]), r[2][3]);
+    const float a4 = __builtin_fmaxf(__builtin_fmaxf(r[3][0], r[3][1]), r[3][2]);
+    const float b0 = __builtin_fmaxf(__builtin_fmaxf(a0, a1), a2);
+    const float b1 = __builtin_fmaxf(__builtin_fmaxf(a3, a4), r[3][3]);
+    x[it] = __builtin_fmaxf(b0, b1);
+    grow_any |= x[it] > st.m_grow[it];
   }
   if (__builtin_expect(__builtin_amdgcn_ballot_w64(grow_any) == 0, 1)) return false;
+  float m[kIT];
+#pragma unroll
+  for (int it = 0; it < kIT; ++it) m[it] = row_max4(x[it]);
   // rare: some row's max grew by more than the slack; rows that did not grow get
   // alpha = 1 (their m is kept)
 #pragma unroll
@@ -275,8 +281,8 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   // ---- DMA geometry: instruction j of this wave fills LDS bytes
   // [(j*kWaves + wave)*1024, +1024) of a tile = rows 4q .. 4q+3, lane -> (row, chunk)
   const int64_t row_bytes = p.k_ss * 2;
-  const char* kbase = reinterpret_cast<const char*>(p.k + b * p.k_sb + (int64_t)kvh * kD);
-  const char* vbase = reinterpret_cast<const char*>(p.v + b * p.k_sb + (int64_t)kvh * kD);
+  const char* kbase = uniform_ptr(p.k + b * p.k_sb + (int64_t)kvh * kD);
+  const char* vbase = uniform_ptr(p.v + b * p.k_sb + (int64_t)kvh * kD);
   // Per-lane byte offsets within a tile (row * row_bytes + swizzled chunk) are
   // loop invariants; the LDS destination of each instruction is wave-uniform.
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);

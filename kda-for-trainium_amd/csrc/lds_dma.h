@@ -26,6 +26,13 @@ __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t
                "s"(reinterpret_cast<const void*>(u)), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
 }
+// A pointer that is the same in every lane, held in scalar registers.
+__device__ __forceinline__ const char* uniform_ptr(const void* ptr) {
+  const uint64_t v = reinterpret_cast<uint64_t>(ptr);
+  return reinterpret_cast<const char*>(
+      ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32)) << 32) |
+      (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v));
+}
 // Same with a per-lane 64-bit address.
 __device__ __forceinline__ void dma16_ptr(const void* src, uint32_t lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
