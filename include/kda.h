@@ -94,10 +94,8 @@ enum {
 };
 
 /* Workspace bytes for operator `op` at the given sizes (unused sizes: 0);
- * -1 for an unknown op or a negative size.  The sizes do not depend on the
- * device, except KDA_OP_SWIGLU_BF16 (an optional workspace whose split-K tail is
- * planned for the current device's compute-unit count: query it with the device
- * current that will run the call; one that is too small only disables the split). */
+ * -1 for an unknown op or a negative size.  The sizes depend only on the
+ * arguments, not on the device. */
 int64_t kda_workspace_size(int op, int64_t batch, int64_t m, int64_t k, int64_t n, int64_t r);
 
 /* ---------------------------------------------------------------- bf16 GEMMs
@@ -141,8 +139,8 @@ int kda_rmsnorm_matmul_bf16_noalloc(const kda_bf16* x, const kda_bf16* gamma, co
  * w_down [F,K].  h is caller-provided scratch of M*F bf16 (the gated activation,
  * written by the first kernel and read by the second).  `workspace` (optional:
  * NULL or too small disables it) of kda_workspace_size(KDA_OP_SWIGLU_BF16, 1, M,
- * K, F, 0) bytes lets the down GEMM split F in two when its output tiles fill at
- * most half the device (fp32 partials, summed into y).  Argument order follows
+ * K, F, 0) = 8*M*K bytes lets the down GEMM split F in two when its output tiles
+ * fill at most half the device (fp32 partials, summed into y).  Argument order follows
  * kernel(v1=x, v2=w_up, v3=w_down, v4=w_gate) of workspaces/swiglu/runs/swiglu_v1.py:38-146. */
 int kda_swiglu_bf16(const kda_bf16* x, const kda_bf16* w_up, const kda_bf16* w_down,
                     const kda_bf16* w_gate, kda_bf16* h, kda_bf16* y, int64_t m, int64_t k,

@@ -54,6 +54,18 @@ def test_invalid_arguments_rejected_without_launch():
         _lib.call("kda_silu_f32", None, None, 16, None)
 
 
+def test_workspace_sizes_are_host_arithmetic():
+    """Size queries touch no device: the documented closed forms, and -1 for an
+    unknown op or a negative size."""
+    q = lambda *a: _lib.query("kda_workspace_size", *a)
+    m, k, f = 2048, 4096, 14336
+    assert q(_lib.OP_SWIGLU_BF16, 1, m, k, f, 0) == 8 * m * k          # down-GEMM fp32 partials
+    assert q(_lib.OP_RMSNORM_MATMUL_BF16, 1, 4096, 4096, 11008, 0) == 2 * 4096 * 4096 + 4 * 4096
+    assert q(_lib.OP_SWIGLU_BF16, 1, m, k, f, 0) == q(_lib.OP_SWIGLU_BF16, 1, m, k, 2 * f, 0)
+    assert q(99, 1, 1, 1, 1, 0) == -1
+    assert q(_lib.OP_MATMUL_F32, 1, -1, 32, 32, 0) == -1
+
+
 def test_ops_reject_cpu_tensors():
     import torch
     from kda import ops
