@@ -1028,6 +1028,20 @@ UpSplit plan_up(int64_t m, int64_t f) {
 }
 
 int64_t workspace_bytes(int op, int64_t b, int64_t m, int64_t k, int64_t n, int64_t r) {
+  // Every size term below is a product of at most three of the arguments times a
+  // small constant.  Sizes whose three largest arguments multiply to more than
+  // 2^40 elements (terabytes: beyond any device) have no workspace; below that no
+  // product or sum here can overflow.
+  if (b < 0 || m < 0 || k < 0 || n < 0 || r < 0) return -1;
+  {
+    double top[3] = {1.0, 1.0, 1.0};
+    for (const int64_t d : {b, m, k, n, r}) {
+      double v = d < 1 ? 1.0 : (double)d;
+      for (int i = 0; i < 3; ++i)
+        if (v > top[i]) { const double t = top[i]; top[i] = v; v = t; }
+    }
+    if (top[0] * top[1] * top[2] > (double)(int64_t(1) << 40)) return -1;
+  }
   Carve c{nullptr};
   switch (op) {
     case KDA_OP_MATMUL_F32:

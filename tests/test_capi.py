@@ -64,6 +64,8 @@ def test_workspace_sizes_are_host_arithmetic():
     assert q(_lib.OP_SWIGLU_BF16, 1, m, k, f, 0) == q(_lib.OP_SWIGLU_BF16, 1, m, k, 2 * f, 0)
     assert q(99, 1, 1, 1, 1, 0) == -1
     assert q(_lib.OP_MATMUL_F32, 1, -1, 32, 32, 0) == -1
+    assert q(_lib.OP_MATMUL_F32, 1, 1 << 40, 1 << 40, 8, 0) == -1     # beyond any device: no overflow
+    assert q(_lib.OP_BMM_SOFTMAX_F32, 1 << 30, 0, 64, 1 << 30, 0) == -1
 
 
 def test_ops_reject_cpu_tensors():
