@@ -46,7 +46,11 @@ constexpr int kBN = 64;       // keys per tile
 constexpr int kWaves = 8;     // per workgroup: HPW query heads x (8 / HPW) blocks of 32 rows
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTileBytes = kBN * kD * 2;                    // one K or V tile: 16 KiB
-constexpr int kDmaPerWave = kTileBytes / (kWaves * 1024);   // DMA instructions per wave per tile
+// The K/V DMAs are issued by waves 0-3 only: they are served first by the
+// instruction arbiter of their SIMDs and otherwise wait at the barrier for the
+// second wave of each SIMD, so the issue work moves off the slower waves.
+constexpr int kDmaWaves = kWaves / 2;
+constexpr int kDmaPerWave = kTileBytes / (kDmaWaves * 1024);   // DMA instructions per issuing wave per tile
 constexpr int kDT = kD / 16 + 1;                            // O^T tiles: 8 of d + the row sums
 constexpr float kLazy = 8.0f;  // running-max slack (log2 units) before O is rescaled
 constexpr int kRing = 4;       // K and V tile slots in LDS (a power of two: slot = kt & 3)
@@ -278,8 +282,8 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
     }
   }
 
-  // ---- DMA geometry: instruction j of this wave fills LDS bytes
-  // [(j*kWaves + wave)*1024, +1024) of a tile = rows 4q .. 4q+3, lane -> (row, chunk)
+  // ---- DMA geometry: instruction j of issuing wave w (< kDmaWaves) fills LDS
+  // bytes [(j*kDmaWaves + w)*1024, +1024) of a tile = rows 4q .. 4q+3, lane -> (row, chunk)
   const int64_t row_bytes = p.k_ss * 2;
   const char* kbase = uniform_ptr(p.k + b * p.k_sb + (int64_t)kvh * kD);
   const char* vbase = uniform_ptr(p.v + b * p.k_sb + (int64_t)kvh * kD);
@@ -290,7 +294,7 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   uint32_t kcol[kDmaPerWave], vcol[kDmaPerWave], koff[kDmaPerWave], voff[kDmaPerWave];
 #pragma unroll
   for (int j = 0; j < kDmaPerWave; ++j) {
-    const int r = (j * kWaves + wave) * 4 + (lane >> 4);
+    const int r = (j * kDmaWaves + wave % kDmaWaves) * 4 + (lane >> 4);
     const int t = lane & 15;
     drow[j] = r;
     kcol[j] = (uint32_t)((t ^ kswz(r)) << 4);
@@ -302,18 +306,19 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   // last key: their scores are masked and their V rows meet p = 0.
   auto issue = [&](const char* base, const uint32_t (&col)[kDmaPerWave],
                    const uint32_t (&off)[kDmaPerWave], int kt, uint32_t lds) {
+    if (wave_u >= kDmaWaves) return;
     const int j0 = kt * kBN;
     const char* tb = base + (int64_t)j0 * row_bytes;
     if (j0 + kBN <= p.seq) {
 #pragma unroll
       for (int j = 0; j < kDmaPerWave; ++j)
-        dma16(tb, off[j], lds + (uint32_t)((j * kWaves + wave_u) * 1024));
+        dma16(tb, off[j], lds + (uint32_t)((j * kDmaWaves + wave_u) * 1024));
     } else {
       const int last = p.seq - 1 - j0;
 #pragma unroll
       for (int j = 0; j < kDmaPerWave; ++j)
         dma16(tb, (uint32_t)(min(drow[j], last) * row_bytes) + col[j],
-              lds + (uint32_t)((j * kWaves + wave_u) * 1024));
+              lds + (uint32_t)((j * kDmaWaves + wave_u) * 1024));
     }
   };
   auto k_tile = [&](int kt) { return smem + (kt % kRing) * kTileBytes; };
@@ -419,6 +424,9 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   }
   rescale(any);
   accumulate_pv(st, v_tile(nkt - 1), pf, lane);
+  // The last fetches (repeats of the last tile into slots no longer read) must
+  // land before the workgroup exits and its LDS is handed to another workgroup.
+  wait_vmcnt<0>();
 
   // ---- normalise and store: lane holds out[row][d = dt*16 + 4g .. +4]; the row
   // sum of its query row is in every element of the ninth O^T tile
