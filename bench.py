@@ -159,6 +159,38 @@ NKIBENCH = {
 }
 
 
+# ----------------------------------------------------------------- extensions
+# bf16 forms of the fused residual RMSNorm operators at the RMSNorm->matmul shape,
+# reported beside the graded configurations (not part of the headline value).
+EXTENSIONS = {
+    "add_rmsnorm_matmul_bf16": dict(desc="x,z[4096,4096] w[4096,11008] g[4096] bf16, eps 1e-6",
+                                    bound="mfma", work=_mm(4096, 4096, 11008)),
+    "matmul_add_rmsnorm_bf16": dict(desc="x[4096,4096] w[4096,11008] z[4096,11008] g[11008] bf16, eps 1e-6",
+                                    bound="mfma", work=_mm(4096, 4096, 11008)),
+}
+
+
+def make_ext_case(name, dev, seed=0):
+    import torch
+    from kda import ops
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    BF = torch.bfloat16
+
+    def normal(shape, std=1.0, mean=0.0):
+        return (torch.randn(shape, generator=g, device=dev) * std + mean).to(BF)
+
+    M, K, N = 4096, 4096, 11008
+    x, w = normal((M, K)), normal((K, N), std=0.02)
+    if name == "add_rmsnorm_matmul_bf16":
+        z, gg = normal((M, K)), normal((K,), std=0.1, mean=1.0)
+        return (lambda i: ops.add_rmsnorm_matmul(x, w, 1e-6, z, gg)), [x, w, z, gg]
+    if name == "matmul_add_rmsnorm_bf16":
+        z, gg = normal((M, N)), normal((N,), std=0.1, mean=1.0)
+        return (lambda i: ops.matmul_add_rmsnorm(x, w, 1e-6, z, gg)), [x, w, z, gg]
+    raise KeyError(name)
+
+
 def make_nki_case(name, dev, seed=0):
     """NKIBench-shape fp32 inputs drawn on the GPU (N(0,1); mamba N(0,0.05);
     AdamW v = |N(0,1)|).  Memory-bound ops rotate input sets larger than the
@@ -360,6 +392,8 @@ def run_cases(cases, reps, dev):
             fn, keep = (lambda i: dst.copy_(src)), [src, dst]
         elif name.startswith("nki:"):
             fn, keep = make_nki_case(name[4:], dev)
+        elif name.startswith("ext:"):
+            fn, keep = make_ext_case(name[4:], dev)
         else:
             fn, keep = make_gpu_case(name, dev)
         torch.cuda.synchronize()
@@ -389,9 +423,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the host numpy baseline")
     ap.add_argument("--nki", default=",".join(NKIBENCH),
                     help="comma-separated NKIBench-shape ops to report beside the configs ('' for none)")
+    ap.add_argument("--ext", default=",".join(EXTENSIONS),
+                    help="comma-separated bf16 residual-RMSNorm extensions to report ('' for none)")
     ap.add_argument("--run", default=None,
                     help="profiling mode: run the comma-separated cases --reps times each and exit "
-                         "(config names, nki:<op>, or copy:<MiB> for a device-to-device copy of "
+                         "(config names, nki:<op>, ext:<op>, or copy:<MiB> for a device-to-device copy of "
                          "known size, the reference for counter scaling)")
     ap.add_argument("--reps", type=int, default=3)
     args = ap.parse_args()
@@ -475,9 +511,22 @@ def main():
             f"frac={rl['frac']:.3f}  cpu={row.get('cpu_p50_ms')} ms")
         nki[n] = row
 
+    ext = {}
+    for n in [x for x in args.ext.split(",") if x]:
+        cfg = EXTENSIONS[n]
+        fn, keep = make_ext_case(n, dev)
+        t = harness.time_op(fn, warmup=args.op_warmup, iters=args.iters, device=dev)
+        rl = harness.roofline(cfg["work"], t.p50_ms * 1e-3, cfg["bound"])
+        ext[n] = dict(shape=cfg["desc"], p50_ms=round(t.p50_ms, 5), bound=cfg["bound"],
+                      achieved=round(rl["achieved"], 1), unit=rl["unit"], roofline_frac=round(rl["frac"], 4))
+        log(f"[bench] ext {n:24s} p50={t.p50_ms * 1e3:9.1f} us  {rl['achieved']:8.1f} {rl['unit']}  "
+            f"frac={rl['frac']:.3f}")
+        del fn, keep
+        torch.cuda.empty_cache()
+
     if not names:
-        # only NKIBench-shape operators were requested: no headline line to build
-        print(json.dumps({"nkibench": nki}), flush=True)
+        # only NKIBench-shape operators or extensions were requested: no headline line to build
+        print(json.dumps({"nkibench": nki, "extensions": ext}), flush=True)
         return 0
     speedups = {n: cpu[n]["p50_ms"] / results[n]["p50_ms"] for n in names if n in cpu}
     geo = harness.geomean(list(speedups.values())) if speedups else None
@@ -518,6 +567,7 @@ def main():
                         seed0_passed=(cpu[n]["passed"] if n in cpu else None))
                 for n in names},
         "nkibench": nki or None,
+        "extensions": ext or None,
         "nkibench_geomean_speedup": (harness.geomean([r["speedup_vs_numpy"] for r in nki.values()])
                                      if nki and not args.no_cpu else None),
     }

@@ -90,7 +90,9 @@ enum {
   KDA_OP_RMSNORM_MATMUL_BF16 = 9,
   KDA_OP_BMM_SOFTMAX_F32 = 10,
   KDA_OP_GQA_F32 = 11,            /* batch = B, m = S, k = Hq, n = Hkv */
-  KDA_OP_SWIGLU_BF16 = 12         /* m = M, k = K: optional split-K partials */
+  KDA_OP_SWIGLU_BF16 = 12,        /* m = M, k = K: optional split-K partials */
+  KDA_OP_ADD_RMSNORM_MATMUL_BF16 = 13,
+  KDA_OP_MATMUL_ADD_RMSNORM_BF16 = 14
 };
 
 /* Workspace bytes for operator `op` at the given sizes (unused sizes: 0);
@@ -118,6 +120,28 @@ int kda_matmul_bf16(const kda_bf16* a, const kda_bf16* b, kda_bf16* c, int64_t m
 int kda_rmsnorm_matmul_bf16(const kda_bf16* x, const kda_bf16* gamma, const kda_bf16* w,
                             kda_bf16* y, int64_t m, int64_t k, int64_t n, float eps,
                             void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The residual variant of kda_rmsnorm_matmul_bf16, in the argument order of
+ * forward(x, w, eps, z, g) of workspaces/add_rmsnorm_matmul/runs/add_rmsnorm_matmul_v1.py:8-146
+ * (fp32 there): y = x + z (summed in fp32, not rounded); out[M,N] =
+ * (y / sqrt(sum_k(y^2 / K) + eps) * g) @ w with x, z [M,K], g [K], w [K,N].  The
+ * pre-pass reads x and z once and writes 1/rms and bf16(y * g); the GEMM applies
+ * 1/rms in its epilogue.  Workspace: KDA_OP_ADD_RMSNORM_MATMUL_BF16 (2*M*K + 4*M
+ * bytes, as KDA_OP_RMSNORM_MATMUL_BF16). */
+int kda_add_rmsnorm_matmul_bf16(const kda_bf16* x, const kda_bf16* w, float eps, const kda_bf16* z,
+                                const kda_bf16* g, kda_bf16* out, int64_t m, int64_t k, int64_t n,
+                                void* workspace, int64_t workspace_bytes, void* stream);
+
+/* y = x @ w + z; out[M,N] = y * g / sqrt(mean_n(y^2) + eps) with x [M,K], w [K,N],
+ * z [M,N], g [N], all bf16; argument order of forward(x, w, eps, z, g) of
+ * workspaces/matmul_add_rmsnorm/runs/matmul_add_rmsnorm_v2_bf16_split.py:8-212
+ * (fp32 there).  The GEMM epilogue adds z to the fp32 accumulators, writes
+ * bf16(y) into out and per-row partial sums of the fp32 y^2; a row kernel then
+ * scales out in place (so y is rounded to bf16 once before the scaling).
+ * Workspace: KDA_OP_MATMUL_ADD_RMSNORM_BF16 (4*M*ceil(N/32) bytes). */
+int kda_matmul_add_rmsnorm_bf16(const kda_bf16* x, const kda_bf16* w, float eps, const kda_bf16* z,
+                                const kda_bf16* g, kda_bf16* out, int64_t m, int64_t k, int64_t n,
+                                void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Bytes of the per-device static buffer behind kda_rmsnorm_matmul_bf16_noalloc. */
 #define KDA_NOALLOC_SCRATCH_BYTES (64LL << 20)

@@ -77,6 +77,7 @@ enum class Epi {
   kStoreF32,       // fp32 C
   kSwiGLUF32,      // fp32 H = silu(acc_gate) * acc_up
   kAddZSsqF32,     // fp32 C = acc + z; part[m][n/64] = sum over the 64 columns of C^2
+  kAddZSsqBf16,    // bf16 C = acc + z (bf16 z); part as above, from the fp32 sums
 };
 
 // One K-segment: A_s (M x k), B_s (k x N) (and B2_s for two-B kernels).
@@ -93,8 +94,8 @@ struct Params {
   int nseg;
   void* c;                 // c[m*ldc + n]  (bf16, or fp32 for the *F32 epilogues)
   const float* row_scale;  // [M]                      (kRowScale)
-  const float* z;          // z[m*ldc + n], fp32       (kAddZSsqF32)
-  float* part;             // part[m*(N/64) + n/64]    (kAddZSsqF32)
+  const void* z;           // z[m*ldc + n], fp32 or bf16 as C   (kAddZSsq*)
+  float* part;             // part[m*(N/WN) + n/WN]             (kAddZSsq*)
   int64_t ldc;
   int64_t batch_a, batch_b, batch_c;   // per-batch strides (elements), batch = blockIdx.y
   int m, n, k;             // k = sum of segment extents
@@ -391,52 +392,87 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(Params p) {
 
   // ---- epilogue: lane holds C[row][col .. col+3] for each 16x16 tile
   const int col_in = (lane >> 4) * 4;
+  // The residual epilogues read z.  Loads and stores complete through one
+  // in-order counter, so a z load issued after a store of C would also wait for
+  // that store: z is loaded ZI tile rows at a time (64 VGPRs) before any of
+  // those rows is stored.
+  constexpr bool kZ = EPI == Epi::kAddZSsqF32 || EPI == Epi::kAddZSsqBf16;
+  constexpr int ZW = EPI == Epi::kAddZSsqF32 ? 4 : 2;   // 32-bit words of z per lane and tile
+  constexpr int ZI = !kZ ? 1 : (64 / (TN * ZW) < TM ? 64 / (TN * ZW) : TM);
+  static_assert(TM % ZI == 0, "z batches");
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int gm = m0 + wm * WM + i * 16 + (lane & 15);
-    const bool row_ok = gm < M;
-    float scale = 1.0f;
-    if constexpr (EPI == Epi::kRowScale) scale = row_ok ? p.row_scale[gm] : 0.f;
-    float ssq = 0.f;
+  for (int i0 = 0; i0 < TM; i0 += ZI) {
+    uint32_t zb[ZI][TN][ZW];
+    if constexpr (kZ) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int gn = n0 + wn * WN + j * 16 + col_in;
-      const bool ok = row_ok && gn < N;
-      float v[4];
+      for (int ii = 0; ii < ZI; ++ii) {
+        const int gm = m0 + wm * WM + (i0 + ii) * 16 + (lane & 15);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if constexpr (EPI == Epi::kSwiGLU || EPI == Epi::kSwiGLUF32)
-          v[r] = silu_f(acc[0][i][j][r]) * acc[NB - 1][i][j][r];
-        else
-          v[r] = acc[0][i][j][r] * scale;
-      }
-      const int64_t off = bz * p.batch_c + (int64_t)gm * p.ldc + gn;
-      if constexpr (EPI == Epi::kAddZSsqF32) {
-        if (ok) {
-          const floatx4 zz = *reinterpret_cast<const floatx4*>(p.z + off);
+        for (int j = 0; j < TN; ++j) {
+          const int gn = n0 + wn * WN + j * 16 + col_in;
+          const int64_t off = bz * p.batch_c + (int64_t)gm * p.ldc + gn;
+          if (gm < M && gn < N) {
+            if constexpr (ZW == 4) {
+              const u32x4 t = *reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(p.z) + off);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            v[r] += zz[r];
-            ssq = fmaf(v[r], v[r], ssq);
+              for (int w = 0; w < 4; ++w) zb[ii][j][w] = t[w];
+            } else {
+              const u32x2 t = *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint16_t*>(p.z) + off);
+              zb[ii][j][0] = t[0];
+              zb[ii][j][1] = t[1];
+            }
+          } else {
+#pragma unroll
+            for (int w = 0; w < ZW; ++w) zb[ii][j][w] = 0u;
           }
         }
       }
-      if (!ok) continue;
-      if constexpr (EPI == Epi::kStoreF32 || EPI == Epi::kSwiGLUF32 || EPI == Epi::kAddZSsqF32) {
-        *reinterpret_cast<floatx4*>(reinterpret_cast<float*>(p.c) + off) =
-            floatx4{v[0], v[1], v[2], v[3]};
-      } else {
-        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.c) + off) =
-            u32x2{pack2(v[0], v[1]), pack2(v[2], v[3])};
-      }
     }
-    if constexpr (EPI == Epi::kAddZSsqF32) {
-      // the 4 lanes l, l+16, l+32, l+48 hold the wave's WN columns of this row
-      ssq += __shfl_xor(ssq, 16);
-      ssq += __shfl_xor(ssq, 32);
-      const int chunk = (n0 + wn * WN) / WN;
-      if (row_ok && lane < 16 && n0 + wn * WN < N)
-        p.part[(int64_t)gm * ((N + WN - 1) / WN) + chunk] = ssq;
+#pragma unroll
+    for (int ii = 0; ii < ZI; ++ii) {
+      const int i = i0 + ii;
+      const int gm = m0 + wm * WM + i * 16 + (lane & 15);
+      const bool row_ok = gm < M;
+      float scale = 1.0f;
+      if constexpr (EPI == Epi::kRowScale) scale = row_ok ? p.row_scale[gm] : 0.f;
+      float ssq = 0.f;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int gn = n0 + wn * WN + j * 16 + col_in;
+        const bool ok = row_ok && gn < N;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if constexpr (EPI == Epi::kSwiGLU || EPI == Epi::kSwiGLUF32)
+            v[r] = silu_f(acc[0][i][j][r]) * acc[NB - 1][i][j][r];
+          else
+            v[r] = acc[0][i][j][r] * scale;
+          if constexpr (EPI == Epi::kAddZSsqF32) v[r] += __builtin_bit_cast(float, zb[ii][j][r]);
+          if constexpr (EPI == Epi::kAddZSsqBf16)
+            v[r] += bf16_bits_to_f32(r & 1 ? zb[ii][j][r >> 1] >> 16 : zb[ii][j][r >> 1] & 0xffffu);
+        }
+        if (!ok) continue;
+        if constexpr (kZ) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) ssq = fmaf(v[r], v[r], ssq);
+        }
+        const int64_t off = bz * p.batch_c + (int64_t)gm * p.ldc + gn;
+        if constexpr (EPI == Epi::kStoreF32 || EPI == Epi::kSwiGLUF32 || EPI == Epi::kAddZSsqF32) {
+          *reinterpret_cast<floatx4*>(reinterpret_cast<float*>(p.c) + off) =
+              floatx4{v[0], v[1], v[2], v[3]};
+        } else {
+          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.c) + off) =
+              u32x2{pack2(v[0], v[1]), pack2(v[2], v[3])};
+        }
+      }
+      if constexpr (kZ) {
+        // the 4 lanes l, l+16, l+32, l+48 hold the wave's WN columns of this row
+        ssq += __shfl_xor(ssq, 16);
+        ssq += __shfl_xor(ssq, 32);
+        const int chunk = (n0 + wn * WN) / WN;
+        if (row_ok && lane < 16 && n0 + wn * WN < N)
+          p.part[(int64_t)gm * ((N + WN - 1) / WN) + chunk] = ssq;
+      }
     }
   }
 }
@@ -676,12 +712,13 @@ __global__ __launch_bounds__(kRowThreads) void rms_split_f32_kernel(
 }
 
 // Row normalisation after a GEMM whose epilogue wrote y = x@w + z into `out` and
-// per-64-column sums of y^2 into part[M][ceil(N/64)]:
+// per-WN-column sums of y^2 into part[M][nchunk]:
 //   out[m, n] = y[m, n] * g[n] / sqrt(sum_n y^2 / N + eps)
-__global__ __launch_bounds__(kRowThreads) void row_rmsnorm_f32_kernel(
-    float* __restrict__ out, const float* __restrict__ part, const float* __restrict__ g, int n,
-    int nchunk, float eps) {
-  const int row = blockIdx.x;
+// One workgroup per row; both forms stream at the device's copy rate (a variant
+// holding the row in registers so that every load precedes the first store
+// measured the same).
+__device__ __forceinline__ float row_rms(const float* __restrict__ part, int row, int nchunk,
+                                         int n, float eps) {
   const int tid = threadIdx.x;
   float s = 0.f;
   for (int c = tid; c < nchunk; c += kRowThreads) s += part[(int64_t)row * nchunk + c];
@@ -693,10 +730,17 @@ __global__ __launch_bounds__(kRowThreads) void row_rmsnorm_f32_kernel(
   float t = 0.f;
 #pragma unroll
   for (int w = 0; w < kRowThreads / 64; ++w) t += wpart[w];
-  const float rms = sqrtf(t / (float)n + eps);
-  floatx4* orow = reinterpret_cast<floatx4*>(out + (int64_t)row * n);
+  return sqrtf(t / (float)n + eps);
+}
+
+// fp32 rows, N % 4 == 0.
+__global__ __launch_bounds__(kRowThreads) void row_rmsnorm_f32_kernel(
+    float* __restrict__ out, const float* __restrict__ part, const float* __restrict__ g, int n,
+    int nchunk, float eps) {
+  const float rms = row_rms(part, blockIdx.x, nchunk, n, eps);
+  floatx4* orow = reinterpret_cast<floatx4*>(out + (int64_t)blockIdx.x * n);
   const floatx4* gr = reinterpret_cast<const floatx4*>(g);
-  for (int c = tid; c < n / 4; c += kRowThreads) {
+  for (int c = threadIdx.x; c < n / 4; c += kRowThreads) {
     floatx4 v = orow[c];
     const floatx4 gg = gr[c];
 #pragma unroll
@@ -705,15 +749,51 @@ __global__ __launch_bounds__(kRowThreads) void row_rmsnorm_f32_kernel(
   }
 }
 
+// The bf16 form: the GEMM epilogue wrote bf16(y) into `out` and the fp32 sums of
+// y^2 into part; out[m, n] = bf16(bf16(y[m, n]) * g[n] / rms), g bf16, N % 8 == 0.
+__global__ __launch_bounds__(kRowThreads) void row_rmsnorm_bf16_kernel(
+    uint16_t* __restrict__ out, const float* __restrict__ part, const uint16_t* __restrict__ g,
+    int n, int nchunk, float eps) {
+  const float rms = row_rms(part, blockIdx.x, nchunk, n, eps);
+  u32x4* orow = reinterpret_cast<u32x4*>(out + (int64_t)blockIdx.x * n);
+  const u32x4* gr = reinterpret_cast<const u32x4*>(g);
+  for (int c = threadIdx.x; c < n / 8; c += kRowThreads) {
+    const u32x4 v = orow[c], gg = gr[c];
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = pack_bf16x2(bf16_bits_to_f32(v[e] & 0xffffu) * bf16_bits_to_f32(gg[e] & 0xffffu) / rms,
+                         bf16_bits_to_f32(v[e] >> 16) * bf16_bits_to_f32(gg[e] >> 16) / rms);
+    orow[c] = o;
+  }
+}
+
 // ---------------------------------------------------------------- RMSNorm pre-pass
-// One workgroup per row: inv_rms[m] = 1/sqrt(mean_k x[m,k]^2 + eps) (fp32 sum of
-// squares of the bf16 values) and xg[m,k] = bf16(x[m,k] * gamma[k]).  x is read
-// once; xg stays in the 256 MB Infinity Cache for the GEMM that follows.
+// One workgroup per row: y = x (+ z when ADD, summed in fp32),
+// inv_rms[m] = 1/sqrt(mean_k y[m,k]^2 + eps) (fp32 sum of squares) and
+// xg[m,k] = bf16(y[m,k] * gamma[k]).  x (and z) are read once; xg stays in the
+// 256 MB Infinity Cache for the GEMM that follows.
 // 128 threads per row measured 11.6 us against 13.8 with 256 (4096 x 4096; 64: 12.1).
 constexpr int kPrepThreads = 128;
 constexpr int kPrepVec = 4;   // 16-byte chunks per thread held in registers (K <= 4096)
 
+// The 8 values of a 16-byte bf16 chunk as fp32 (x, plus z when ADD).
+template <bool ADD>
+__device__ __forceinline__ void prep_values(const u32x4& xv, const u32x4& zv, float (&y)[8]) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    y[2 * w] = bf16_bits_to_f32(xv[w] & 0xffffu);
+    y[2 * w + 1] = bf16_bits_to_f32(xv[w] >> 16);
+    if constexpr (ADD) {
+      y[2 * w] += bf16_bits_to_f32(zv[w] & 0xffffu);
+      y[2 * w + 1] += bf16_bits_to_f32(zv[w] >> 16);
+    }
+  }
+}
+
+template <bool ADD>
 __global__ __launch_bounds__(kPrepThreads) void rms_prep_kernel(const uint16_t* __restrict__ x,
+                                                                const uint16_t* __restrict__ z,
                                                                 const uint16_t* __restrict__ gamma,
                                                                 uint16_t* __restrict__ xg,
                                                                 float* __restrict__ inv_rms, int k,
@@ -722,68 +802,58 @@ __global__ __launch_bounds__(kPrepThreads) void rms_prep_kernel(const uint16_t* 
   const int tid = threadIdx.x;
   const int nchunk = k / 8;
   const u32x4* xr = reinterpret_cast<const u32x4*>(x + (int64_t)row * k);
-  u32x4 v[kPrepVec];
+  const u32x4* zr = ADD ? reinterpret_cast<const u32x4*>(z + (int64_t)row * k) : nullptr;
+  const u32x4 zero{0u, 0u, 0u, 0u};
+  u32x4 v[kPrepVec], vz[kPrepVec];
   float ssq = 0.f;
 #pragma unroll
   for (int u = 0; u < kPrepVec; ++u) {
     const int c = tid + u * kPrepThreads;
-    v[u] = (c < nchunk) ? __builtin_nontemporal_load(xr + c) : u32x4{0u, 0u, 0u, 0u};
+    v[u] = (c < nchunk) ? __builtin_nontemporal_load(xr + c) : zero;
+    vz[u] = (ADD && c < nchunk) ? __builtin_nontemporal_load(zr + c) : zero;
+    float y[8];
+    prep_values<ADD>(v[u], vz[u], y);
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float lo = __builtin_bit_cast(float, v[u][w] << 16);
-      const float hi = __builtin_bit_cast(float, v[u][w] & 0xffff0000u);
-      ssq = fmaf(lo, lo, ssq);
-      ssq = fmaf(hi, hi, ssq);
-    }
+    for (int e = 0; e < 8; ++e) ssq = fmaf(y[e], y[e], ssq);
   }
-  // tail chunks beyond the register-held part (K > 8192)
+  // tail chunks beyond the register-held part (K > 4096)
   for (int c = tid + kPrepVec * kPrepThreads; c < nchunk; c += kPrepThreads) {
-    const u32x4 t = xr[c];
+    float y[8];
+    prep_values<ADD>(xr[c], ADD ? zr[c] : zero, y);
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float lo = __builtin_bit_cast(float, t[w] << 16);
-      const float hi = __builtin_bit_cast(float, t[w] & 0xffff0000u);
-      ssq = fmaf(lo, lo, ssq);
-      ssq = fmaf(hi, hi, ssq);
-    }
+    for (int e = 0; e < 8; ++e) ssq = fmaf(y[e], y[e], ssq);
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) ssq += __shfl_xor(ssq, off);
   __shared__ float part[kPrepThreads / 64];
-  __shared__ float s_inv;
   if ((tid & 63) == 0) part[tid >> 6] = ssq;
   __syncthreads();
   if (tid == 0) {
     float s = 0.f;
 #pragma unroll
     for (int w = 0; w < kPrepThreads / 64; ++w) s += part[w];
-    const float inv = 1.0f / sqrtf(s / (float)k + eps);
-    s_inv = inv;
-    inv_rms[row] = inv;
+    inv_rms[row] = 1.0f / sqrtf(s / (float)k + eps);
   }
-  __syncthreads();
-  (void)s_inv;
   const u32x4* gr = reinterpret_cast<const u32x4*>(gamma);
   u32x4* outr = reinterpret_cast<u32x4*>(xg + (int64_t)row * k);
-  auto scale_store = [&](const u32x4& t, int c) {
+  auto scale_store = [&](const u32x4& t, const u32x4& tz, int c) {
     const u32x4 g = gr[c];
+    float y[8];
+    prep_values<ADD>(t, tz, y);
     u32x4 o;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float x0 = __builtin_bit_cast(float, t[w] << 16);
-      const float x1 = __builtin_bit_cast(float, t[w] & 0xffff0000u);
-      const float g0 = __builtin_bit_cast(float, g[w] << 16);
-      const float g1 = __builtin_bit_cast(float, g[w] & 0xffff0000u);
-      o[w] = pack2(x0 * g0, x1 * g1);
-    }
+    for (int w = 0; w < 4; ++w)
+      o[w] = pack2(y[2 * w] * bf16_bits_to_f32(g[w] & 0xffffu),
+                   y[2 * w + 1] * bf16_bits_to_f32(g[w] >> 16));
     outr[c] = o;
   };
 #pragma unroll
   for (int u = 0; u < kPrepVec; ++u) {
     const int c = tid + u * kPrepThreads;
-    if (c < nchunk) scale_store(v[u], c);
+    if (c < nchunk) scale_store(v[u], vz[u], c);
   }
-  for (int c = tid + kPrepVec * kPrepThreads; c < nchunk; c += kPrepThreads) scale_store(xr[c], c);
+  for (int c = tid + kPrepVec * kPrepThreads; c < nchunk; c += kPrepThreads)
+    scale_store(xr[c], ADD ? zr[c] : zero, c);
 }
 
 
@@ -1064,7 +1134,11 @@ int64_t workspace_bytes(int op, int64_t b, int64_t m, int64_t k, int64_t n, int6
       plan_swiglu(c, m, k, n);
       break;
     case KDA_OP_RMSNORM_MATMUL_BF16:
+    case KDA_OP_ADD_RMSNORM_MATMUL_BF16:
       plan_rms_bf16(c, m, k);
+      break;
+    case KDA_OP_MATMUL_ADD_RMSNORM_BF16:  // row partials of the sum of squares
+      c.take<float>(m * ((n + 31) / 32));
       break;
     case KDA_OP_BMM_SOFTMAX_F32:   // two fp16 limb planes of rhs^T [B][N][64], tile scales [B][N/64]
       c.take<uint16_t>(2 * b * n * 64 + 2 * b * ((n + 63) / 64));
@@ -1113,30 +1187,91 @@ extern "C" int kda_matmul_bf16(const kda_bf16* a, const kda_bf16* b, kda_bf16* c
   return launch_auto<true, Epi::kStore>(p, 1, as_stream(stream), "matmul_bf16");
 }
 
-extern "C" int kda_rmsnorm_matmul_bf16(const kda_bf16* x, const kda_bf16* gamma, const kda_bf16* w,
-                                       kda_bf16* y, int64_t m, int64_t k, int64_t n, float eps,
-                                       void* workspace, int64_t workspace_bytes_, void* stream) {
-  clear_error();
-  const char* what = "rmsnorm_matmul_bf16";
+namespace {
+// RMSNorm -> matmul on bf16 operands, with the residual z added first when given:
+// a pre-pass writes bf16((x (+ z)) * gamma) and 1/rms per row into the workspace,
+// and the GEMM applies 1/rms in its epilogue.
+int rms_matmul_bf16(const char* what, int op, const kda_bf16* x, const kda_bf16* z,
+                    const kda_bf16* gamma, const kda_bf16* w, kda_bf16* y, int64_t m, int64_t k,
+                    int64_t n, float eps, void* workspace, int64_t ws_bytes, void* stream) {
   if (int rc = validate(what, x, w, y, m, n, k)) return rc;
   if (k == 0) return set_error(KDA_ERR_INVALID_ARG, "%s: K must be > 0", what);
   if (!gamma || !aligned16(gamma))
     return set_error(KDA_ERR_INVALID_ARG, "%s: gamma null or not 16-byte aligned", what);
+  if (op == KDA_OP_ADD_RMSNORM_MATMUL_BF16 && (!z || !aligned16(z)))
+    return set_error(KDA_ERR_INVALID_ARG, "%s: z null or not 16-byte aligned", what);
   if (!(eps >= 0.f)) return set_error(KDA_ERR_INVALID_ARG, "%s: eps must be >= 0", what);
   if (m == 0 || n == 0) return KDA_OK;
-  if (int rc = check_ws(what, workspace, workspace_bytes_,
-                        workspace_bytes(KDA_OP_RMSNORM_MATMUL_BF16, 1, m, k, n, 0)))
-    return rc;
+  if (int rc = check_ws(what, workspace, ws_bytes, workspace_bytes(op, 1, m, k, n, 0))) return rc;
   Carve cv{reinterpret_cast<uint8_t*>(workspace)};
   const RmsBf16Plan wp = plan_rms_bf16(cv, m, k);
   hipStream_t st = as_stream(stream);
-  hipLaunchKernelGGL(rms_prep_kernel, dim3((unsigned)m), dim3(kPrepThreads), 0, st, x, gamma, wp.xg,
-                     wp.inv, (int)k, eps);
-  if (int rc = check_launch("rmsnorm_matmul_bf16(prep)")) return rc;
+  if (op == KDA_OP_ADD_RMSNORM_MATMUL_BF16)
+    hipLaunchKernelGGL(rms_prep_kernel<true>, dim3((unsigned)m), dim3(kPrepThreads), 0, st, x, z,
+                       gamma, wp.xg, wp.inv, (int)k, eps);
+  else
+    hipLaunchKernelGGL(rms_prep_kernel<false>, dim3((unsigned)m), dim3(kPrepThreads), 0, st, x,
+                       nullptr, gamma, wp.xg, wp.inv, (int)k, eps);
+  if (int rc = check_launch(what)) return rc;
   Params p = make_params(m, n, y, n);
   p.row_scale = wp.inv;
   add_seg(p, wp.xg, k, w, n, k);
   return launch_auto<true, Epi::kRowScale>(p, 1, st, what);
+}
+}  // namespace
+
+extern "C" int kda_rmsnorm_matmul_bf16(const kda_bf16* x, const kda_bf16* gamma, const kda_bf16* w,
+                                       kda_bf16* y, int64_t m, int64_t k, int64_t n, float eps,
+                                       void* workspace, int64_t workspace_bytes_, void* stream) {
+  clear_error();
+  return rms_matmul_bf16("rmsnorm_matmul_bf16", KDA_OP_RMSNORM_MATMUL_BF16, x, nullptr, gamma, w,
+                         y, m, k, n, eps, workspace, workspace_bytes_, stream);
+}
+
+extern "C" int kda_add_rmsnorm_matmul_bf16(const kda_bf16* x, const kda_bf16* w, float eps,
+                                           const kda_bf16* z, const kda_bf16* g, kda_bf16* out,
+                                           int64_t m, int64_t k, int64_t n, void* workspace,
+                                           int64_t workspace_bytes_, void* stream) {
+  clear_error();
+  return rms_matmul_bf16("add_rmsnorm_matmul_bf16", KDA_OP_ADD_RMSNORM_MATMUL_BF16, x, z, g, w,
+                         out, m, k, n, eps, workspace, workspace_bytes_, stream);
+}
+
+extern "C" int kda_matmul_add_rmsnorm_bf16(const kda_bf16* x, const kda_bf16* w, float eps,
+                                           const kda_bf16* z, const kda_bf16* g, kda_bf16* out,
+                                           int64_t m, int64_t k, int64_t n, void* workspace,
+                                           int64_t workspace_bytes_, void* stream) {
+  clear_error();
+  const char* what = "matmul_add_rmsnorm_bf16";
+  if (int rc = validate(what, x, w, out, m, n, k)) return rc;
+  if (!z || !g || !aligned16(z) || !aligned16(g))
+    return set_error(KDA_ERR_INVALID_ARG, "%s: z and g must be non-null and 16-byte aligned", what);
+  if (!(eps >= 0.f)) return set_error(KDA_ERR_INVALID_ARG, "%s: eps must be >= 0", what);
+  if (m == 0 || n == 0) return KDA_OK;
+  if (k == 0) return set_error(KDA_ERR_INVALID_ARG, "%s: K must be > 0", what);
+  if (int rc = check_ws(what, workspace, workspace_bytes_,
+                        workspace_bytes(KDA_OP_MATMUL_ADD_RMSNORM_BF16, 1, m, k, n, 0)))
+    return rc;
+  hipStream_t st = as_stream(stream);
+  Carve cv{reinterpret_cast<uint8_t*>(workspace)};
+  float* part = cv.take<float>(m * ((n + 31) / 32));
+  // The epilogue writes bf16(x@w + z) into out and per-wave-tile sums of the
+  // fp32 (x@w + z)^2; the row pass scales out in place.  256-wide N tiles give
+  // 64-column partials, 128-wide ones (when 256-wide tiles would leave CUs
+  // idle) 32-column partials.
+  Params p = make_params(m, n, out, n);
+  add_seg(p, x, k, w, n, k);
+  p.z = z;
+  p.part = part;
+  const int64_t tiles256 = ((m + 255) / 256) * ((n + 255) / 256);
+  const bool narrow = tiles256 < device_cu_count();
+  const int64_t nchunk = narrow ? (n + 31) / 32 : (n + 63) / 64;
+  if (int rc = narrow ? launch_n<256, 128, 1, true, Epi::kAddZSsqBf16, 1, 64, 2>(p, 1, st, what)
+                      : launch_n<256, 256, 1, true, Epi::kAddZSsqBf16, 1>(p, 1, st, what))
+    return rc;
+  hipLaunchKernelGGL(row_rmsnorm_bf16_kernel, dim3((unsigned)m), dim3(kRowThreads), 0, st, out,
+                     part, g, (int)n, (int)nchunk, eps);
+  return check_launch(what);
 }
 
 // ---- allocation-free RMSNorm -> matmul -------------------------------------

@@ -39,6 +39,8 @@ SIGNATURES = {
     "kda_rmsnorm_matmul_f32": [_p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
     "kda_add_rmsnorm_matmul_f32": [_p, _p, _f32, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
     "kda_matmul_add_rmsnorm_f32": [_p, _p, _f32, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
+    "kda_add_rmsnorm_matmul_bf16": [_p, _p, _f32, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
+    "kda_matmul_add_rmsnorm_bf16": [_p, _p, _f32, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
     "kda_swiglu_f32": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p],
     "kda_bmm_softmax_f32": [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "kda_mamba_f32": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
@@ -68,6 +70,8 @@ OP_RMSNORM_MATMUL_BF16 = 9
 OP_BMM_SOFTMAX_F32 = 10
 OP_GQA_F32 = 11
 OP_SWIGLU_BF16 = 12
+OP_ADD_RMSNORM_MATMUL_BF16 = 13
+OP_MATMUL_ADD_RMSNORM_BF16 = 14
 
 
 class KdaError(RuntimeError):

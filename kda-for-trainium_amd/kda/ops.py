@@ -342,41 +342,51 @@ def rmsnorm_matmul_workspace_size(m: int, k: int) -> int:
 
 def add_rmsnorm_matmul(x: torch.Tensor, w: torch.Tensor, eps: float, z: torch.Tensor,
                        g: torch.Tensor, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """y = x + z; out = (y / sqrt(sum(y^2 / K) + eps) * g) @ w, fp32.
+    """y = x + z; out = (y / sqrt(sum(y^2 / K) + eps) * g) @ w.
 
-    x, z (M, K), w (K, N), g (K,).  Argument order of forward(x, w, eps, z, g)
+    x, z (M, K), w (K, N), g (K,), all fp32 or all bf16 (output in the same dtype).
+    fp32: the reference operator (three-product bf16 split).  bf16: y is summed in
+    fp32, a pre-pass writes bf16(y * g) and 1/rms, the GEMM applies 1/rms in its
+    epilogue.  Argument order of forward(x, w, eps, z, g)
     (workspaces/add_rmsnorm_matmul/docs/draft-phase1.md:10-24; kernel
     workspaces/add_rmsnorm_matmul/runs/add_rmsnorm_matmul_v1.py:8-146).
     """
-    _same_dtype(("x", x), ("w", w), ("z", z), ("g", g))
-    _check("x", x, F32, ndim=2)
+    dt = _same_dtype(("x", x), ("w", w), ("z", z), ("g", g))
+    _check("x", x, dt, ndim=2)
     m, k, n = _gemm_dims("x", x, "w", w)
-    _check("z", z, F32, shape=(m, k))
-    _check("g", g, F32, shape=(k,))
-    out = torch.empty((m, n), dtype=F32, device=x.device)
-    ws = _workspace(workspace, workspace_size(_lib.OP_ADD_RMSNORM_MATMUL_F32, 1, m, k, n), x.device)
-    _lib.call("kda_add_rmsnorm_matmul_f32", x.data_ptr(), w.data_ptr(), float(eps), z.data_ptr(),
-              g.data_ptr(), out.data_ptr(), m, k, n, ws.data_ptr(), ws.numel(), _stream(x))
+    _check("z", z, dt, shape=(m, k))
+    _check("g", g, dt, shape=(k,))
+    out = torch.empty((m, n), dtype=dt, device=x.device)
+    op, fn = ((_lib.OP_ADD_RMSNORM_MATMUL_F32, "kda_add_rmsnorm_matmul_f32") if dt == F32 else
+              (_lib.OP_ADD_RMSNORM_MATMUL_BF16, "kda_add_rmsnorm_matmul_bf16"))
+    ws = _workspace(workspace, workspace_size(op, 1, m, k, n), x.device)
+    _lib.call(fn, x.data_ptr(), w.data_ptr(), float(eps), z.data_ptr(), g.data_ptr(),
+              out.data_ptr(), m, k, n, ws.data_ptr(), ws.numel(), _stream(x))
     return out
 
 
 def matmul_add_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, z: torch.Tensor,
                        g: torch.Tensor, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """y = x @ w + z; out = y * g / sqrt(mean_n(y^2) + eps), fp32.
+    """y = x @ w + z; out = y * g / sqrt(mean_n(y^2) + eps).
 
-    x (M, K), w (K, N), z (M, N), g (N,).  Argument order of forward(x, w, eps, z, g)
-    (workspaces/matmul_add_rmsnorm/docs/draft-phase1.md:10-22; kernel
-    workspaces/matmul_add_rmsnorm/runs/matmul_add_rmsnorm_v2_bf16_split.py:8-212).
+    x (M, K), w (K, N), z (M, N), g (N,), all fp32 or all bf16 (output in the same
+    dtype).  The GEMM epilogue adds z and writes per-row partial sums of y^2 (from
+    the fp32 accumulators); a row kernel applies the norm in place (bf16: y is
+    rounded to bf16 once before that scaling).  Argument order of
+    forward(x, w, eps, z, g) (workspaces/matmul_add_rmsnorm/docs/draft-phase1.md:10-22;
+    kernel workspaces/matmul_add_rmsnorm/runs/matmul_add_rmsnorm_v2_bf16_split.py:8-212).
     """
-    _same_dtype(("x", x), ("w", w), ("z", z), ("g", g))
-    _check("x", x, F32, ndim=2)
+    dt = _same_dtype(("x", x), ("w", w), ("z", z), ("g", g))
+    _check("x", x, dt, ndim=2)
     m, k, n = _gemm_dims("x", x, "w", w)
-    _check("z", z, F32, shape=(m, n))
-    _check("g", g, F32, shape=(n,))
-    out = torch.empty((m, n), dtype=F32, device=x.device)
-    ws = _workspace(workspace, workspace_size(_lib.OP_MATMUL_ADD_RMSNORM_F32, 1, m, k, n), x.device)
-    _lib.call("kda_matmul_add_rmsnorm_f32", x.data_ptr(), w.data_ptr(), float(eps), z.data_ptr(),
-              g.data_ptr(), out.data_ptr(), m, k, n, ws.data_ptr(), ws.numel(), _stream(x))
+    _check("z", z, dt, shape=(m, n))
+    _check("g", g, dt, shape=(n,))
+    out = torch.empty((m, n), dtype=dt, device=x.device)
+    op, fn = ((_lib.OP_MATMUL_ADD_RMSNORM_F32, "kda_matmul_add_rmsnorm_f32") if dt == F32 else
+              (_lib.OP_MATMUL_ADD_RMSNORM_BF16, "kda_matmul_add_rmsnorm_bf16"))
+    ws = _workspace(workspace, workspace_size(op, 1, m, k, n), x.device)
+    _lib.call(fn, x.data_ptr(), w.data_ptr(), float(eps), z.data_ptr(), g.data_ptr(),
+              out.data_ptr(), m, k, n, ws.data_ptr(), ws.numel(), _stream(x))
     return out
 
 

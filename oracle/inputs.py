@@ -13,7 +13,8 @@ Two families:
   and AdamW's v = |N(0,1)| (workspaces/adamw/docs/plan-phase1.md:233-234).
   Unlike the reference's adapter, each seed really draws different inputs.
 * Graded configurations (SiLU fp32, RMSNorm->matmul bf16, SwiGLU bf16, AdamW
-  fp32, causal GQA bf16).  Distributions as specified per configuration; the
+  fp32, causal GQA bf16), and the two residual RMSNorm variants at the
+  RMSNorm->matmul shape in bf16.  Distributions as specified per configuration; the
   generator is ``np.random.default_rng(seed)`` (float32 ``standard_normal``,
   scaled), chosen over the legacy generator for speed at 10^8-element sizes.
   bf16 inputs are drawn in fp32 and rounded once to bf16 (RNE); the GPU and the
@@ -51,6 +52,8 @@ PARAMS = {
     # graded configurations
     "silu_cfg": ["x"],
     "rmsnorm_matmul_cfg": ["x", "gamma", "w", "eps"],
+    "add_rmsnorm_matmul_cfg": ["x", "w", "eps", "z", "g"],
+    "matmul_add_rmsnorm_cfg": ["x", "w", "eps", "z", "g"],
     "swiglu_cfg": ["x", "w_up", "w_down", "w_gate"],
     "adamw_cfg": ["param", "grad", "m", "v"],
     "gqa_cfg": ["q", "k", "v"],
@@ -75,12 +78,15 @@ DIMS = {
     "gqa_full": dict(B=1, S=4096, HQ=16, HKV=8, D=128),
     "silu_cfg": dict(M=2048, N=8192),
     "rmsnorm_matmul_cfg": dict(M=4096, K=4096, N=11008),
+    "add_rmsnorm_matmul_cfg": dict(M=4096, K=4096, N=11008),
+    "matmul_add_rmsnorm_cfg": dict(M=4096, K=4096, N=11008),
     "swiglu_cfg": dict(M=2048, K=4096, F=14336),
     "adamw_cfg": dict(N=1 << 27),
     "gqa_cfg": dict(B=4, S=4096, HQ=32, HKV=8, D=128),
 }
 
-EPS = {"add_rmsnorm_matmul": 1e-5, "matmul_add_rmsnorm": 1e-5, "rmsnorm_matmul_cfg": 1e-6}
+EPS = {"add_rmsnorm_matmul": 1e-5, "matmul_add_rmsnorm": 1e-5, "rmsnorm_matmul_cfg": 1e-6,
+       "add_rmsnorm_matmul_cfg": 1e-6, "matmul_add_rmsnorm_cfg": 1e-6}
 
 # AdamW configuration hyper-parameters.
 ADAMW_CFG = dict(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01, step=10)
@@ -160,6 +166,20 @@ def draw(case: str, seed: int, dims: Optional[Dict[str, int]] = None) -> Dict[st
         gamma = to_bf16_rne(_rng_normal(rng, (K,), mean=1.0, std=0.1))
         w = to_bf16_rne(_rng_normal(rng, (K, N), std=0.02))
         return {"x": x, "gamma": gamma, "w": w, "eps": EPS[case]}
+    if case == "add_rmsnorm_matmul_cfg":
+        M, K, N = d["M"], d["K"], d["N"]
+        x = to_bf16_rne(_rng_normal(rng, (M, K)))
+        z = to_bf16_rne(_rng_normal(rng, (M, K)))
+        g = to_bf16_rne(_rng_normal(rng, (K,), mean=1.0, std=0.1))
+        w = to_bf16_rne(_rng_normal(rng, (K, N), std=0.02))
+        return {"x": x, "w": w, "eps": EPS[case], "z": z, "g": g}
+    if case == "matmul_add_rmsnorm_cfg":
+        M, K, N = d["M"], d["K"], d["N"]
+        x = to_bf16_rne(_rng_normal(rng, (M, K)))
+        w = to_bf16_rne(_rng_normal(rng, (K, N), std=0.02))
+        z = to_bf16_rne(_rng_normal(rng, (M, N)))
+        g = to_bf16_rne(_rng_normal(rng, (N,), mean=1.0, std=0.1))
+        return {"x": x, "w": w, "eps": EPS[case], "z": z, "g": g}
     if case == "swiglu_cfg":
         M, K, F = d["M"], d["K"], d["F"]
         x = to_bf16_rne(_rng_normal(rng, (M, K)))

@@ -62,6 +62,9 @@ def test_workspace_sizes_are_host_arithmetic():
     assert q(_lib.OP_SWIGLU_BF16, 1, m, k, f, 0) == 8 * m * k          # down-GEMM fp32 partials
     assert q(_lib.OP_RMSNORM_MATMUL_BF16, 1, 4096, 4096, 11008, 0) == 2 * 4096 * 4096 + 4 * 4096
     assert q(_lib.OP_SWIGLU_BF16, 1, m, k, f, 0) == q(_lib.OP_SWIGLU_BF16, 1, m, k, 2 * f, 0)
+    assert q(_lib.OP_ADD_RMSNORM_MATMUL_BF16, 1, 4096, 4096, 11008, 0) == 2 * 4096 * 4096 + 4 * 4096
+    assert q(_lib.OP_MATMUL_ADD_RMSNORM_BF16, 1, 4096, 4096, 11008, 0) == 4 * 4096 * (11008 // 32)
+    assert q(_lib.OP_MATMUL_ADD_RMSNORM_BF16, 1, 7, 4096, 40, 0) == 4 * 7 * 2
     assert q(99, 1, 1, 1, 1, 0) == -1
     assert q(_lib.OP_MATMUL_F32, 1, -1, 32, 32, 0) == -1
     assert q(_lib.OP_MATMUL_F32, 1, 1 << 40, 1 << 40, 8, 0) == -1     # beyond any device: no overflow

@@ -1,4 +1,5 @@
-"""GPU parity: bf16 MFMA GEMMs (plain, RMSNorm-fused, SwiGLU) vs the fp32 oracle.
+"""GPU parity: bf16 MFMA GEMMs (plain, RMSNorm-fused with and without a residual,
+SwiGLU) vs the fp32 oracle.
 
 Inputs are bf16 values; the oracle computes in fp32 on the same values.  Gate:
 relative-L2 <= 1e-2 for bf16 operators (the kernels land near 1e-3: bf16
@@ -75,6 +76,74 @@ def test_rmsnorm_matmul_row_scale_invariance(dev):
     g = to_dev(d["gamma"], dev, BF)
     y0 = to_host(ops.rmsnorm_matmul(to_dev(d["x"], dev, BF), to_dev(d["w"], dev, BF), gamma=g))
     y1 = to_host(ops.rmsnorm_matmul(to_dev(x, dev, BF), to_dev(d["w"], dev, BF), gamma=g))
+    np.testing.assert_array_equal(y0, y1)
+
+
+def _residual_args(d, dev):
+    return [to_dev(d["x"], dev, BF), to_dev(d["w"], dev, BF), d["eps"], to_dev(d["z"], dev, BF),
+            to_dev(d["g"], dev, BF)]
+
+
+@pytest.mark.parametrize("case,fn,ref", [
+    ("add_rmsnorm_matmul_cfg", ops.add_rmsnorm_matmul, oo.add_rmsnorm_matmul),
+    ("matmul_add_rmsnorm_cfg", ops.matmul_add_rmsnorm, oo.matmul_add_rmsnorm)])
+def test_residual_rmsnorm_config_full_size_all_seeds(dev, case, fn, ref):
+    # the fused residual variants at the RMSNorm->matmul shape (4096 x 4096 x 11008)
+    for s in SEEDS:
+        d = oi.draw(case, s)
+        got = fn(*_residual_args(d, dev))
+        assert got.dtype == BF
+        err = rel_l2(to_host(got), ref(**d))
+        print(f"{case} seed={s} rel_l2={err:.3e}", flush=True)
+        assert err < BF16_GATE
+
+
+RAGGED_RESIDUAL = [dict(M=256, K=64, N=128), dict(M=77, K=136, N=56), dict(M=1, K=8, N=8),
+                   dict(M=513, K=1000, N=264), dict(M=300, K=200, N=1000),
+                   # K past what the norm pre-pass holds in registers (4096)
+                   dict(M=40, K=5000, N=72),
+                   # enough 256 x 256 tiles to take the wide (64-column partial) path
+                   dict(M=2048, K=256, N=8192)]
+
+
+@pytest.mark.parametrize("dims", RAGGED_RESIDUAL)
+@pytest.mark.parametrize("case,fn,ref", [
+    ("add_rmsnorm_matmul_cfg", ops.add_rmsnorm_matmul, oo.add_rmsnorm_matmul),
+    ("matmul_add_rmsnorm_cfg", ops.matmul_add_rmsnorm, oo.matmul_add_rmsnorm)])
+def test_residual_rmsnorm_ragged(dev, case, fn, ref, dims):
+    d = oi.draw(case, 6, dims=dims)
+    err = rel_l2(to_host(fn(*_residual_args(d, dev))), ref(**d))
+    print(f"{case} {dims} rel_l2={err:.3e}", flush=True)
+    assert err < 5e-3
+
+
+def test_add_rmsnorm_matmul_reduces_to_rmsnorm_matmul(dev):
+    # z = 0: the same pre-pass arithmetic and GEMM as rmsnorm_matmul (bit for bit);
+    # x and z swapped: the fp32 sum commutes (bit for bit)
+    d = oi.draw("add_rmsnorm_matmul_cfg", 7, dims=dict(M=300, K=520, N=264))
+    x, w, eps, z, g = _residual_args(d, dev)
+    zero = torch.zeros_like(z)
+    a = to_host(ops.add_rmsnorm_matmul(x, w, eps, zero, g))
+    b = to_host(ops.rmsnorm_matmul(x, w, gamma=g, eps=eps))
+    np.testing.assert_array_equal(a, b)
+    np.testing.assert_array_equal(to_host(ops.add_rmsnorm_matmul(x, w, eps, z, g)),
+                                  to_host(ops.add_rmsnorm_matmul(z, w, eps, x, g)))
+
+
+def test_matmul_add_rmsnorm_bf16_row_properties(dev):
+    d = oi.draw("matmul_add_rmsnorm_cfg", 8, dims=dict(M=512, K=384, N=1032))
+    x, w, _, z, g = _residual_args(d, dev)
+    ones = torch.ones_like(g)
+    # g = 1, eps = 0: every output row has unit mean square (up to bf16 rounding)
+    out = to_host(ops.matmul_add_rmsnorm(x, w, 0.0, z, ones)).astype(np.float64)
+    ms = np.mean(out * out, axis=1)
+    assert np.max(np.abs(ms - 1.0)) < 1e-2, np.max(np.abs(ms - 1.0))
+    # scaling a row of x and z by a power of two leaves its output row unchanged
+    xs, zs = d["x"].copy(), d["z"].copy()
+    xs[::5] *= 4.0
+    zs[::5] *= 4.0
+    y0 = to_host(ops.matmul_add_rmsnorm(x, w, 0.0, z, g))
+    y1 = to_host(ops.matmul_add_rmsnorm(to_dev(xs, dev, BF), w, 0.0, to_dev(zs, dev, BF), g))
     np.testing.assert_array_equal(y0, y1)
 
 
