@@ -23,15 +23,21 @@
 //   then holds 4 keys of query row (l & 15) per 16x16 tile.  K rows are read in a
 //   permuted order so that, per 32-key chunk, each lane's 8 probabilities are 8
 //   consecutive keys -> they form the B operand of O^T += V^T P^T directly
-//   (no LDS round trip for P).  A ninth O^T tile multiplies P by ones: it
-//   accumulates the row sums of the same bf16 probabilities on the MFMA.
-//   Online softmax in fp32: p = exp2(s*scale*log2e - m*scale*log2e) (one FMA and
-//   one v_exp_f32); the running max is raised lazily (only when a tile max exceeds
-//   it by more than 2^kLazy), so O is rescaled only then.  Masking is applied only
-//   on tiles that cross the causal diagonal or the sequence end.
-//   Software pipeline: iteration kt issues the MFMAs of O += V(kt-1) P(kt-1) and
-//   S(kt+1) = K(kt+1) Q^T in the same basic block as the softmax VALU work of
-//   S(kt), so a wave's MFMAs execute while it issues its VALU work.
+//   (no LDS round trip for P).  Row sums of the probabilities are kept per lane
+//   in fp32 (16 keys of a row per lane and tile) and reduced across the row's
+//   four lanes once, at the end.
+//   Online softmax in fp32 on log2-scaled scores: Q is multiplied by
+//   scale*log2(e) (and rounded to bf16) once when it is loaded, and each S^T
+//   accumulator starts from -m, the running max of its row, so the MFMAs produce
+//   s*scale*log2e - m directly and p = exp2(acc) is one v_exp_f32 per score.  The
+//   running max is raised lazily (only when a tile's scores exceed it by more
+//   than kLazy), so O is rescaled only then.  Masking is applied only on tiles
+//   that cross the causal diagonal or the sequence end.
+//   Software pipeline, per iteration kt: the MFMAs of O += V(kt-1) P(kt-1) run in
+//   one basic block with the row-max test of S(kt); after the (rarely taken)
+//   running-max update, the MFMAs of S(kt+1) = K(kt+1) Q^T run in one basic
+//   block with the exponentials of S(kt).  A wave's MFMAs execute while it
+//   issues its VALU work.
 #include "common.h"
 #include "lanes.h"
 #include "lds_dma.h"
@@ -51,7 +57,7 @@ constexpr int kTileBytes = kBN * kD * 2;                    // one K or V tile: 
 // second wave of each SIMD, so the issue work moves off the slower waves.
 constexpr int kDmaWaves = kWaves / 2;
 constexpr int kDmaPerWave = kTileBytes / (kDmaWaves * 1024);   // DMA instructions per issuing wave per tile
-constexpr int kDT = kD / 16 + 1;                            // O^T tiles: 8 of d + the row sums
+constexpr int kDT = kD / 16;                                // O^T tiles along d
 constexpr float kLazy = 8.0f;  // running-max slack (log2 units) before O is rescaled
 constexpr int kRing = 4;       // K and V tile slots in LDS (a power of two: slot = kt & 3)
 
@@ -80,11 +86,10 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 
 // Per-wave state carried across key tiles.
 struct State {
-  bf16x8 qf[kIT][4];      // Q fragments (MFMA B operand): row it*16 + l16, d = dc*32 + 8g .. +8
-  floatx4 o[kIT][kDT];    // O^T: lane holds row l16, d = dt*16 + 4g + r; tile 8 = row sums
-  float m[kIT];           // running max (raw score units)
-  float m_grow[kIT];      // m + kLazy / scale_log2: a tile max above it raises m
-  float shift[kIT];       // m * scale_log2 (0 while m = -inf)
+  bf16x8 qf[kIT][4];      // Q * scale*log2e (MFMA B operand): row it*16 + l16, d = dc*32 + 8g .. +8
+  floatx4 o[kIT][kDT];    // O^T: lane holds row l16, d = dt*16 + 4g + r
+  float l[kIT];           // this lane's part of the row sum of the probabilities
+  floatx4 c0[kIT];        // S^T accumulator seed: -m (the row's running max, log2 units)
 };
 
 __device__ __forceinline__ bf16x8 k_frag(const uint8_t* kt_lds, int t, int dc, int lane) {
@@ -94,14 +99,10 @@ __device__ __forceinline__ bf16x8 k_frag(const uint8_t* kt_lds, int t, int dc, i
                                           (((dc * 4 + g) ^ kswz(krow)) << 4));
 }
 
-// S^T = K Q^T: s[it][t], t = 2c + hh covers keys 32c + 8a + 4hh + r for A-row 4a + r.
-// d-chunk outer: the 8 accumulators rotate, consecutive MFMAs are independent.
+// S^T = K Q^T - m: s[it][t], t = 2c + hh covers keys 32c + 8a + 4hh + r for A-row
+// 4a + r.  d-chunk outer: the 8 accumulators rotate, consecutive MFMAs are independent.
 __device__ __forceinline__ void scores(const State& st, const uint8_t* k_lds, int lane,
                                        floatx4 (&s)[kIT][4]) {
-#pragma unroll
-  for (int it = 0; it < kIT; ++it)
-#pragma unroll
-    for (int t = 0; t < 4; ++t) s[it][t] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int dc = 0; dc < 4; ++dc)
 #pragma unroll
@@ -109,41 +110,41 @@ __device__ __forceinline__ void scores(const State& st, const uint8_t* k_lds, in
       const bf16x8 kf = k_frag(k_lds, t, dc, lane);
 #pragma unroll
       for (int it = 0; it < kIT; ++it)
-        s[it][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, st.qf[it][dc], s[it][t], 0, 0, 0);
+        s[it][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, st.qf[it][dc],
+                                                           dc == 0 ? st.c0[it] : s[it][t], 0, 0, 0);
     }
 }
 
-// O^T += V^T P^T (V^T fragment: row d = dt*16 + l16, keys 32c + 8g .. +8), plus the
-// row sums ones^T P^T.
+// O^T += V^T P^T (V^T fragment: row d = dt*16 + l16, keys 32c + 8g .. +8).
+// The 16 V fragments are read kAhead fragments ahead of the MFMAs that use them
+// (in program order, which the scheduler keeps under register pressure), so
+// several LDS reads are in flight instead of one.
+constexpr int kAhead = 2;
 __device__ __forceinline__ void accumulate_pv(State& st, const uint8_t* v_lds,
                                               const bf16x8 (&pf)[kIT][2], int lane) {
+  bf16x8 vf[16];
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
+  for (int f = 0; f < kAhead; ++f) vf[f] = read_mn_frag<kD>(v_lds, (f & 7) * 16, 32 * (f >> 3), lane);
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const bf16x8 vf = read_mn_frag<kD>(v_lds, dt * 16, 32 * c, lane);
-#pragma unroll
-      for (int it = 0; it < kIT; ++it)
-        st.o[it][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[it][c], st.o[it][dt], 0, 0, 0);
-    }
-  bf16x8 ones;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) ones[e] = (__bf16)1.0f;
-#pragma unroll
-  for (int c = 0; c < 2; ++c)
+  for (int f = 0; f < 16; ++f) {
+    if (f + kAhead < 16)
+      vf[f + kAhead] = read_mn_frag<kD>(v_lds, ((f + kAhead) & 7) * 16, 32 * ((f + kAhead) >> 3), lane);
+    const int c = f >> 3, dt = f & 7;
 #pragma unroll
     for (int it = 0; it < kIT; ++it)
-      st.o[it][kDT - 1] =
-          __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[it][c], st.o[it][kDT - 1], 0, 0, 0);
+      st.o[it][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[f], pf[it][c], st.o[it][dt], 0, 0, 0);
+  }
 }
 
-// Online softmax of S(kt), first half: masking, row maxima and the running-max
-// update.  Returns whether the running max of some row was raised; then alpha
-// holds the factor O must be multiplied by and st.shift the new m * scale_log2.
-// The common case (no row grows) costs the max reductions and one compare.
+// Online softmax of S(kt) (accumulators s = t - m in log2 units, t the scaled
+// score, m the row's running max), first half: masking and the row-max test.
+// Returns whether some row of the wave has a score above m + kLazy.  A row's max
+// exceeds kLazy iff one of its four lanes' partial maxima (16 values each, a tree
+// of three-input maxima) does, so the test needs no cross-lane reduction: one
+// compare per row and a ballot.
 template <bool CAUSAL, bool MASK>
-__device__ __forceinline__ bool softmax_stats(State& st, const Args& p, int kt, int w0, int lane,
-                                              floatx4 (&s)[kIT][4], float (&alpha)[kIT]) {
+__device__ __forceinline__ bool softmax_test(const Args& p, int kt, int w0, int lane,
+                                             floatx4 (&s)[kIT][4], float (&x)[kIT]) {
   const int l16 = lane & 15, g = lane >> 4;
   if constexpr (MASK) {
     const int j_base = kt * kBN;
@@ -159,11 +160,6 @@ __device__ __forceinline__ bool softmax_stats(State& st, const Args& p, int kt, 
           if (32 * (t >> 1) + 4 * (t & 1) + r > lim) s[it][t][r] = -INFINITY;
     }
   }
-  // Lane-partial maxima (16 values of each row per lane, a tree of three-input
-  // maxima).  A row's max exceeds its threshold iff one of its four lanes'
-  // partial maxima does (the threshold is the same in the four lanes), so the
-  // common case needs no cross-lane reduction: one compare per row and a ballot.
-  float x[kIT];
   bool grow_any = false;
 #pragma unroll
   for (int it = 0; it < kIT; ++it) {
@@ -176,40 +172,48 @@ __device__ __forceinline__ bool softmax_stats(State& st, const Args& p, int kt, 
     const float b0 = __builtin_fmaxf(__builtin_fmaxf(a0, a1), a2);
     const float b1 = __builtin_fmaxf(__builtin_fmaxf(a3, a4), r[3][3]);
     x[it] = __builtin_fmaxf(b0, b1);
-    grow_any |= x[it] > st.m_grow[it];
+    grow_any |= x[it] > kLazy;
   }
-  if (__builtin_expect(__builtin_amdgcn_ballot_w64(grow_any) == 0, 1)) return false;
-  float m[kIT];
-#pragma unroll
-  for (int it = 0; it < kIT; ++it) m[it] = row_max4(x[it]);
-  // rare: some row's max grew by more than the slack; rows that did not grow get
-  // alpha = 1 (their m is kept)
-#pragma unroll
-  for (int it = 0; it < kIT; ++it) {
-    const bool grow = m[it] > st.m_grow[it];
-    const float m_new = grow ? __builtin_fmaxf(st.m[it], m[it]) : st.m[it];
-    // a row whose keys so far are all masked keeps m = -inf (its O is 0)
-    alpha[it] = (m_new == -INFINITY) ? 1.f
-                                     : __builtin_amdgcn_exp2f((st.m[it] - m_new) * p.scale_log2);
-    st.m[it] = m_new;
-    st.shift[it] = (m_new == -INFINITY) ? 0.f : m_new * p.scale_log2;
-    st.m_grow[it] = m_new + kLazy / p.scale_log2;
-  }
-  return true;
+  return __builtin_amdgcn_ballot_w64(grow_any) != 0;
 }
 
-// Second half: probabilities p = exp2(s*scale_log2 - shift), packed to bf16 as the
-// B operand of O^T += V^T P^T.
-__device__ __forceinline__ void softmax_probs(const State& st, const Args& p,
-                                              const floatx4 (&s)[kIT][4], bf16x8 (&pf)[kIT][2]) {
+// Second half, taken when the test above fires (or for the first tile, with
+// FIRST: m is then set to the tile's row max whatever its value): rows whose max
+// grew get m += delta (delta = their max), their accumulators and seed move by
+// -delta, and alpha = 2^-delta is the factor their O and row sums must be
+// multiplied by; other rows get alpha = 1.  A row whose keys are all masked
+// keeps its m.
+template <bool FIRST>
+__device__ __forceinline__ void softmax_raise(State& st, floatx4 (&s)[kIT][4],
+                                              const float (&x)[kIT], float (&alpha)[kIT]) {
+#pragma unroll
+  for (int it = 0; it < kIT; ++it) {
+    const float m = row_max4(x[it]);
+    const bool grow = FIRST ? (m != -INFINITY) : (m > kLazy);
+    const float delta = grow ? m : 0.f;
+    alpha[it] = grow ? __builtin_amdgcn_exp2f(-delta) : 1.f;
+    // the row sums so far (tiles up to kt-1) move to the new m now, before this
+    // tile's probabilities are added; O (one tile behind) moves in the next
+    // iteration.  The first tile has no sums yet.
+    if constexpr (!FIRST) st.l[it] *= alpha[it];
+    st.c0[it] -= delta;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) s[it][t] -= delta;
+  }
+}
+
+// Probabilities p = exp2(acc), packed to bf16 as the B operand of O^T += V^T P^T.
+__device__ __forceinline__ void softmax_probs(State& st, const floatx4 (&s)[kIT][4],
+                                              bf16x8 (&pf)[kIT][2]) {
 #pragma unroll
   for (int it = 0; it < kIT; ++it) {
     float pv[4][4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < 4; ++t) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        pv[t][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[it][t][r], p.scale_log2, -st.shift[it]));
+      for (int r = 0; r < 4; ++r) pv[t][r] = __builtin_amdgcn_exp2f(s[it][t][r]);
+      st.l[it] += (pv[t][0] + pv[t][1]) + (pv[t][2] + pv[t][3]);
+    }
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       u32x4 w;
@@ -222,16 +226,56 @@ __device__ __forceinline__ void softmax_probs(const State& st, const Args& p,
   }
 }
 
-// Scheduling hint for one steady-state iteration (68 MFMAs next to ~100 VALU and
-// transcendental instructions of the softmax): alternate one MFMA with a few
-// VALU/TRANS instructions, so the softmax issues while the MFMA pipe is busy.
+// Block B of an iteration: the probabilities of S(kt) (held in s) and
+// S(kt+1) = K(kt+1) Q^T - m, key tile by key tile in place: tile t's exps and
+// packs read s[.][t] before the MFMAs of S(kt+1) overwrite it, so S(kt+1) needs
+// no second set of accumulators.
+__device__ __forceinline__ void probs_then_scores(State& st, const uint8_t* k_lds, int lane,
+                                                  floatx4 (&s)[kIT][4], bf16x8 (&pf)[kIT][2]) {
+  uint32_t w[kIT][2][4];
+  // K fragments (t, dc) in order f = 4t + dc, read kAhead ahead of their MFMAs
+  bf16x8 kf[16];
+#pragma unroll
+  for (int f = 0; f < kAhead; ++f) kf[f] = k_frag(k_lds, f >> 2, f & 3, lane);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+#pragma unroll
+    for (int it = 0; it < kIT; ++it) {
+      const floatx4 e{__builtin_amdgcn_exp2f(s[it][t][0]), __builtin_amdgcn_exp2f(s[it][t][1]),
+                      __builtin_amdgcn_exp2f(s[it][t][2]), __builtin_amdgcn_exp2f(s[it][t][3])};
+      w[it][t >> 1][2 * (t & 1)] = pack2(e[0], e[1]);
+      w[it][t >> 1][2 * (t & 1) + 1] = pack2(e[2], e[3]);
+      st.l[it] += (e[0] + e[1]) + (e[2] + e[3]);
+    }
+#pragma unroll
+    for (int dc = 0; dc < 4; ++dc) {
+      const int f = 4 * t + dc;
+      if (f + kAhead < 16) kf[f + kAhead] = k_frag(k_lds, (f + kAhead) >> 2, (f + kAhead) & 3, lane);
+#pragma unroll
+      for (int it = 0; it < kIT; ++it)
+        s[it][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[f], st.qf[it][dc],
+                                                           dc == 0 ? st.c0[it] : s[it][t], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < kIT; ++it)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+      pf[it][c] = __builtin_bit_cast(bf16x8, u32x4{w[it][c][0], w[it][c][1], w[it][c][2], w[it][c][3]});
+}
+
+// Scheduling hint for a block of N MFMAs next to VALU and transcendental work:
+// alternate one MFMA with V VALU/TRANS instructions, so the softmax issues while
+// the MFMA pipe is busy.
+template <int N, int V>
 __device__ __forceinline__ void interleave_hint() {
 #pragma unroll
-  for (int i = 0; i < 68; ++i) {
+  for (int i = 0; i < N; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x402, 2, 0);   // VALU | TRANS
+    __builtin_amdgcn_sched_group_barrier(0x402, V, 0);   // VALU | TRANS
   }
 }
+
 
 // HPW query heads (of one kv head) per workgroup, HPW in {1, 2, 4, 8}: the
 // workgroup covers BM = 32 * 8 / HPW query rows of each of its heads, and a
@@ -262,23 +306,30 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
 
   State st;
   {
+    // Q fragments, scaled by scale*log2(e) and rounded to bf16 once
     const uint16_t* qp = p.q + b * p.q_sb + (int64_t)h * kD;
 #pragma unroll
     for (int it = 0; it < kIT; ++it) {
       const int row = w0 + it * 16 + l16;
 #pragma unroll
-      for (int dc = 0; dc < 4; ++dc)
-        st.qf[it][dc] = (row < p.seq)
-                            ? *reinterpret_cast<const bf16x8*>(qp + row * p.q_ss + dc * 32 + g * 8)
-                            : bf16x8{};
+      for (int dc = 0; dc < 4; ++dc) {
+        const u32x4 raw = (row < p.seq)
+                              ? *reinterpret_cast<const u32x4*>(qp + row * p.q_ss + dc * 32 + g * 8)
+                              : u32x4{0u, 0u, 0u, 0u};
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[e] = pack2(__builtin_bit_cast(float, raw[e] << 16) * p.scale_log2,
+                       __builtin_bit_cast(float, raw[e] & 0xffff0000u) * p.scale_log2);
+        st.qf[it][dc] = __builtin_bit_cast(bf16x8, w);
+      }
     }
 #pragma unroll
     for (int it = 0; it < kIT; ++it) {
 #pragma unroll
       for (int dt = 0; dt < kDT; ++dt) st.o[it][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-      st.m[it] = -INFINITY;
-      st.m_grow[it] = -INFINITY;
-      st.shift[it] = 0.f;
+      st.c0[it] = floatx4{0.f, 0.f, 0.f, 0.f};   // m = 0 until the first tile sets it
+      st.l[it] = 0.f;
     }
   }
 
@@ -290,22 +341,23 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   // Per-lane byte offsets within a tile (row * row_bytes + swizzled chunk) are
   // loop invariants; the LDS destination of each instruction is wave-uniform.
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  int drow[kDmaPerWave];
-  uint32_t kcol[kDmaPerWave], vcol[kDmaPerWave], koff[kDmaPerWave], voff[kDmaPerWave];
+  auto dma_row = [&](int j) { return (j * kDmaWaves + wave % kDmaWaves) * 4 + (lane >> 4); };
+  auto kcol = [&](int r) { return (uint32_t)(((lane & 15) ^ kswz(r)) << 4); };
+  auto vcol = [&](int r) {
+    const int t = lane & 15;
+    return (uint32_t)((((t >> 1) ^ mswz(r)) << 5) + ((t & 1) << 4));
+  };
+  uint32_t koff[kDmaPerWave], voff[kDmaPerWave];
 #pragma unroll
   for (int j = 0; j < kDmaPerWave; ++j) {
-    const int r = (j * kDmaWaves + wave % kDmaWaves) * 4 + (lane >> 4);
-    const int t = lane & 15;
-    drow[j] = r;
-    kcol[j] = (uint32_t)((t ^ kswz(r)) << 4);
-    vcol[j] = (uint32_t)(((((t >> 1) ^ mswz(r)) << 5)) + ((t & 1) << 4));
-    koff[j] = (uint32_t)(r * row_bytes) + kcol[j];
-    voff[j] = (uint32_t)(r * row_bytes) + vcol[j];
+    const int r = dma_row(j);
+    koff[j] = (uint32_t)(r * row_bytes) + kcol(r);
+    voff[j] = (uint32_t)(r * row_bytes) + vcol(r);
   }
   // Rows past the sequence (only in the last, partial tile) are clamped to the
   // last key: their scores are masked and their V rows meet p = 0.
-  auto issue = [&](const char* base, const uint32_t (&col)[kDmaPerWave],
-                   const uint32_t (&off)[kDmaPerWave], int kt, uint32_t lds) {
+  auto issue = [&](const char* base, bool is_v, const uint32_t (&off)[kDmaPerWave], int kt,
+                   uint32_t lds) {
     if (wave_u >= kDmaWaves) return;
     const int j0 = kt * kBN;
     const char* tb = base + (int64_t)j0 * row_bytes;
@@ -316,9 +368,11 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
     } else {
       const int last = p.seq - 1 - j0;
 #pragma unroll
-      for (int j = 0; j < kDmaPerWave; ++j)
-        dma16(tb, (uint32_t)(min(drow[j], last) * row_bytes) + col[j],
+      for (int j = 0; j < kDmaPerWave; ++j) {
+        const int r = dma_row(j);
+        dma16(tb, (uint32_t)(min(r, last) * row_bytes) + (is_v ? vcol(r) : kcol(r)),
               lds + (uint32_t)((j * kDmaWaves + wave_u) * 1024));
+      }
     }
   };
   auto k_tile = [&](int kt) { return smem + (kt % kRing) * kTileBytes; };
@@ -337,14 +391,14 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   // S(kt).  Each DMA has two iterations to land: the barrier that ends iteration
   // kt waits only for the DMAs issued in iteration kt-1 (K(kt+2), V(kt)), which
   // iteration kt+1 reads.
-  issue(kbase, kcol, koff, 0, lds_addr(k_tile(0)));
-  issue(kbase, kcol, koff, min(1, nkt - 1), lds_addr(k_tile(1)));
-  issue(kbase, kcol, koff, min(2, nkt - 1), lds_addr(k_tile(2)));
-  issue(vbase, vcol, voff, 0, lds_addr(v_tile(0)));
+  issue(kbase, false, koff, 0, lds_addr(k_tile(0)));
+  issue(kbase, false, koff, min(1, nkt - 1), lds_addr(k_tile(1)));
+  issue(kbase, false, koff, min(2, nkt - 1), lds_addr(k_tile(2)));
+  issue(vbase, true, voff, 0, lds_addr(v_tile(0)));
   wait_vmcnt<0>();
   __syncthreads();
-  floatx4 s[kIT][4], s_next[kIT][4];
-  bf16x8 pf[kIT][2], pf_next[kIT][2];
+  floatx4 s[kIT][4];
+  bf16x8 pf[kIT][2];
   float alpha[kIT];
   scores(st, k_tile(0), lane, s);
   __syncthreads();
@@ -353,8 +407,8 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   // no longer read, so every iteration issues the same number of DMAs and the
   // wait below has a fixed count.
   auto fetch = [&](int kt) {
-    issue(kbase, kcol, koff, min(kt + 3, nkt - 1), lds_addr(k_tile(kt + 3)));
-    issue(vbase, vcol, voff, min(kt + 1, nkt - 1), lds_addr(v_tile(kt + 1)));
+    issue(kbase, false, koff, min(kt + 3, nkt - 1), lds_addr(k_tile(kt + 3)));
+    issue(vbase, true, voff, min(kt + 1, nkt - 1), lds_addr(v_tile(kt + 1)));
   };
   // O moves to the running max set by the previous tile's statistics; done
   // before the next O += V P (and at the top of an iteration, so the branch does
@@ -368,58 +422,59 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
     }
   };
   auto finish = [&]() {
-#pragma unroll
-    for (int it = 0; it < kIT; ++it) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) s[it][t] = s_next[it][t];
-#pragma unroll
-      for (int c = 0; c < 2; ++c) pf[it][c] = pf_next[it][c];
-    }
     // DMAs still allowed in flight: those issued in this iteration
     wait_vmcnt<2 * kDmaPerWave>();
     __syncthreads();
   };
 
-  // kt = 0: no O update yet (O is 0; its first rescale multiplies zeros)
-  bool any;
+  // kt = 0: no O update yet.  The first tile sets every row's m to its max
+  // (S(0) was computed with m = 0), before S(1) is computed from the new seed.
+  float x[kIT];
+  bool any = false;
   {
     fetch(0);
-    if (nkt > 1) scores(st, k_tile(1), lane, s_next);
-    any = (nfree > 0) ? softmax_stats<CAUSAL, false>(st, p, 0, w0, lane, s, alpha)
-                      : softmax_stats<CAUSAL, true>(st, p, 0, w0, lane, s, alpha);
-    any = false;
-    softmax_probs(st, p, s, pf_next);
+    if (nfree > 0) softmax_test<CAUSAL, false>(p, 0, w0, lane, s, x);
+    else softmax_test<CAUSAL, true>(p, 0, w0, lane, s, x);
+    softmax_raise<true>(st, s, x, alpha);
+    if (nkt > 1) probs_then_scores(st, k_tile(1), lane, s, pf);
+    else softmax_probs(st, s, pf);
     finish();
   }
+  // Iteration body: block A = O += V(kt-1) P(kt-1) (36 MFMAs) with the row-max
+  // test of S(kt); the rare running-max update; block B = the exponentials of
+  // S(kt) with S(kt+1) (32 MFMAs).
   int kt = 1;
   const int n_mid_free = min(nfree, nkt - 1);
   for (; kt < n_mid_free; ++kt) {
     fetch(kt);
     rescale(any);
-    any = softmax_stats<CAUSAL, false>(st, p, kt, w0, lane, s, alpha);
     accumulate_pv(st, v_tile(kt - 1), pf, lane);
-    scores(st, k_tile(kt + 1), lane, s_next);
-    softmax_probs(st, p, s, pf_next);
-    interleave_hint();
+    any = softmax_test<CAUSAL, false>(p, kt, w0, lane, s, x);
+    interleave_hint<36, 1>();
+    if (any) softmax_raise<false>(st, s, x, alpha);
+    probs_then_scores(st, k_tile(kt + 1), lane, s, pf);
+    interleave_hint<32, 2>();
     finish();
   }
   for (; kt < nkt - 1; ++kt) {
     fetch(kt);
     rescale(any);
-    any = softmax_stats<CAUSAL, true>(st, p, kt, w0, lane, s, alpha);
     accumulate_pv(st, v_tile(kt - 1), pf, lane);
-    scores(st, k_tile(kt + 1), lane, s_next);
-    softmax_probs(st, p, s, pf_next);
-    interleave_hint();
+    any = softmax_test<CAUSAL, true>(p, kt, w0, lane, s, x);
+    interleave_hint<36, 2>();
+    if (any) softmax_raise<false>(st, s, x, alpha);
+    probs_then_scores(st, k_tile(kt + 1), lane, s, pf);
+    interleave_hint<32, 2>();
     finish();
   }
   if (kt == nkt - 1 && kt >= 1) {   // last tile: no S(kt+1)
     fetch(kt);
     rescale(any);
-    any = (kt < nfree) ? softmax_stats<CAUSAL, false>(st, p, kt, w0, lane, s, alpha)
-                       : softmax_stats<CAUSAL, true>(st, p, kt, w0, lane, s, alpha);
     accumulate_pv(st, v_tile(kt - 1), pf, lane);
-    softmax_probs(st, p, s, pf_next);
+    any = (kt < nfree) ? softmax_test<CAUSAL, false>(p, kt, w0, lane, s, x)
+                       : softmax_test<CAUSAL, true>(p, kt, w0, lane, s, x);
+    if (any) softmax_raise<false>(st, s, x, alpha);
+    softmax_probs(st, s, pf);
     finish();
   }
   rescale(any);
@@ -428,16 +483,16 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   // land before the workgroup exits and its LDS is handed to another workgroup.
   wait_vmcnt<0>();
 
-  // ---- normalise and store: lane holds out[row][d = dt*16 + 4g .. +4]; the row
-  // sum of its query row is in every element of the ninth O^T tile
+  // ---- normalise and store: lane holds out[row][d = dt*16 + 4g .. +4]; the
+  // row sum is the sum of the four lanes' parts
   uint16_t* op = p.out + b * p.o_sb + (int64_t)h * p.o_sh;
 #pragma unroll
   for (int it = 0; it < kIT; ++it) {
-    const float inv = 1.0f / st.o[it][kDT - 1][0];
+    const float inv = 1.0f / row_sum4(st.l[it]);
     const int row = w0 + it * 16 + l16;
     if (row >= p.seq) continue;
 #pragma unroll
-    for (int dt = 0; dt < kDT - 1; ++dt) {
+    for (int dt = 0; dt < kDT; ++dt) {
       const floatx4 o = st.o[it][dt] * inv;
       u32x2 w;
       w[0] = pack2(o[0], o[1]);
