@@ -116,19 +116,25 @@ __device__ __forceinline__ void scores(const State& st, const uint8_t* k_lds, in
 }
 
 // O^T += V^T P^T (V^T fragment: row d = dt*16 + l16, keys 32c + 8g .. +8).
-// The 16 V fragments are read kAhead fragments ahead of the MFMAs that use them
-// (in program order, which the scheduler keeps under register pressure), so
-// several LDS reads are in flight instead of one.
+// The 16 V fragments are read kAhead fragments ahead of the MFMAs that use them,
+// so several LDS reads are in flight instead of one.  A scheduling barrier that
+// only VALU, SALU and transcendental instructions may cross pins each read and
+// MFMA at its place in program order (left alone, the scheduler sinks every read
+// to just before its first use to save registers, and moves MFMAs above reads).
 constexpr int kAhead = 2;
+constexpr int kPinReads = 0x0002 | 0x0004 | 0x0400;   // VALU, SALU, TRANS may cross
+__device__ __forceinline__ void pin_reads() { __builtin_amdgcn_sched_barrier(kPinReads); }
 __device__ __forceinline__ void accumulate_pv(State& st, const uint8_t* v_lds,
                                               const bf16x8 (&pf)[kIT][2], int lane) {
   bf16x8 vf[16];
 #pragma unroll
   for (int f = 0; f < kAhead; ++f) vf[f] = read_mn_frag<kD>(v_lds, (f & 7) * 16, 32 * (f >> 3), lane);
+  pin_reads();
 #pragma unroll
   for (int f = 0; f < 16; ++f) {
     if (f + kAhead < 16)
       vf[f + kAhead] = read_mn_frag<kD>(v_lds, ((f + kAhead) & 7) * 16, 32 * ((f + kAhead) >> 3), lane);
+    pin_reads();
     const int c = f >> 3, dt = f & 7;
 #pragma unroll
     for (int it = 0; it < kIT; ++it)
@@ -237,6 +243,7 @@ __device__ __forceinline__ void probs_then_scores(State& st, const uint8_t* k_ld
   bf16x8 kf[16];
 #pragma unroll
   for (int f = 0; f < kAhead; ++f) kf[f] = k_frag(k_lds, f >> 2, f & 3, lane);
+  pin_reads();
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -251,6 +258,7 @@ __device__ __forceinline__ void probs_then_scores(State& st, const uint8_t* k_ld
     for (int dc = 0; dc < 4; ++dc) {
       const int f = 4 * t + dc;
       if (f + kAhead < 16) kf[f + kAhead] = k_frag(k_lds, (f + kAhead) >> 2, (f + kAhead) & 3, lane);
+      pin_reads();
 #pragma unroll
       for (int it = 0; it < kIT; ++it)
         s[it][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[f], st.qf[it][dc],
