@@ -312,6 +312,10 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   const int q0 = qb * kBM;
   const int w0 = q0 + (wave / HPW) * kWaveRows;     // this wave's first query row
 
+  // The instruction arbiter serves the older waves (0-3) of each SIMD first, and
+  // they also issue the K/V DMAs; the younger waves get a higher issue priority
+  // so both reach the per-iteration barrier together (1.3 % same-box).
+  if (__builtin_amdgcn_readfirstlane(wave) >= kDmaWaves) __builtin_amdgcn_s_setprio(1);
   State st;
   {
     // Q fragments, scaled by scale*log2(e) and rounded to bf16 once
