@@ -121,7 +121,7 @@ __device__ __forceinline__ void scores(const State& st, const uint8_t* k_lds, in
 // only VALU, SALU and transcendental instructions may cross pins each read and
 // MFMA at its place in program order (left alone, the scheduler sinks every read
 // to just before its first use to save registers, and moves MFMAs above reads).
-constexpr int kAhead = 2;
+constexpr int kAhead = 3;
 constexpr int kPinReads = 0x0002 | 0x0004 | 0x0400;   // VALU, SALU, TRANS may cross
 __device__ __forceinline__ void pin_reads() { __builtin_amdgcn_sched_barrier(kPinReads); }
 __device__ __forceinline__ void accumulate_pv(State& st, const uint8_t* v_lds,
@@ -272,17 +272,6 @@ __device__ __forceinline__ void probs_then_scores(State& st, const uint8_t* k_ld
       pf[it][c] = __builtin_bit_cast(bf16x8, u32x4{w[it][c][0], w[it][c][1], w[it][c][2], w[it][c][3]});
 }
 
-// Scheduling hint for a block of N MFMAs next to VALU and transcendental work:
-// alternate one MFMA with V VALU/TRANS instructions, so the softmax issues while
-// the MFMA pipe is busy.
-template <int N, int V>
-__device__ __forceinline__ void interleave_hint() {
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x402, V, 0);   // VALU | TRANS
-  }
-}
 
 
 // HPW query heads (of one kv head) per workgroup, HPW in {1, 2, 4, 8}: the
@@ -462,10 +451,8 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
     rescale(any);
     accumulate_pv(st, v_tile(kt - 1), pf, lane);
     any = softmax_test<CAUSAL, false>(p, kt, w0, lane, s, x);
-    interleave_hint<36, 1>();
     if (any) softmax_raise<false>(st, s, x, alpha);
     probs_then_scores(st, k_tile(kt + 1), lane, s, pf);
-    interleave_hint<32, 2>();
     finish();
   }
   for (; kt < nkt - 1; ++kt) {
@@ -473,10 +460,8 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
     rescale(any);
     accumulate_pv(st, v_tile(kt - 1), pf, lane);
     any = softmax_test<CAUSAL, true>(p, kt, w0, lane, s, x);
-    interleave_hint<36, 2>();
     if (any) softmax_raise<false>(st, s, x, alpha);
     probs_then_scores(st, k_tile(kt + 1), lane, s, pf);
-    interleave_hint<32, 2>();
     finish();
   }
   if (kt == nkt - 1 && kt >= 1) {   // last tile: no S(kt+1)
