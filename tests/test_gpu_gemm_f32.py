@@ -53,8 +53,11 @@ SMALL = {
     "lora": [dict(M=256, K=64, N=256, R=32), dict(M=77, K=96, N=136, R=64),
              # x@a split along K into 16 and into 2 fp32 partials
              dict(M=512, K=1024, N=256, R=128), dict(M=300, K=640, N=200, R=64)],
-    "rmsnorm_matmul": [dict(M=256, K=128, N=256), dict(M=50, K=96, N=72)],
-    "add_rmsnorm_matmul": [dict(M=256, K=128, N=256), dict(M=50, K=96, N=72)],
+    # K of 2048 and 2560 (several chunks per thread in the norm pass), M not a multiple of 4
+    "rmsnorm_matmul": [dict(M=256, K=128, N=256), dict(M=50, K=96, N=72), dict(M=7, K=2048, N=40),
+                       dict(M=37, K=2560, N=64)],
+    "add_rmsnorm_matmul": [dict(M=256, K=128, N=256), dict(M=50, K=96, N=72), dict(M=5, K=2048, N=40),
+                           dict(M=33, K=2560, N=64)],
     "matmul_add_rmsnorm": [dict(M=256, K=128, N=256), dict(M=50, K=96, N=200), dict(M=300, K=64, N=520)],
     "swiglu": [dict(M=256, K=64, N=128), dict(M=50, K=96, N=160)],
 }
