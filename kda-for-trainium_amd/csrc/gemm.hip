@@ -1628,9 +1628,20 @@ extern "C" int kda_swiglu_f32(const float* x, const float* w_up, const float* w_
   if (int rc = split(x, m * k, sp.xh, sp.xl, st, what)) return rc;
   if (int rc = split(w_gate, k * f, sp.gh, sp.gl, st, what)) return rc;
   if (int rc = split(w_up, k * f, sp.uh, sp.ul, st, what)) return rc;
-  Params up = make_params(m, f, sp.h, f);
+  // Gate/up GEMM: as on the bf16 path, columns that would leave the last round
+  // of 256x128 tiles partly idle (4096 x 3072: 384 tiles, 1.5 rounds on 256 CUs)
+  // run as one round of 128x128 dual-B tiles.
+  const UpSplit us = plan_up(m, f);
+  Params up = make_params(m, us.f_main, sp.h, f);
   add_split_segs(up, sp.xh, sp.xl, k, sp.gh, sp.gl, f, k, sp.uh, sp.ul);
   if (int rc = launch<256, 128, 2, true, Epi::kSwiGLUF32>(up, 1, st, "swiglu_f32(up/gate)")) return rc;
+  if (us.f_tail > 0) {
+    const int64_t c0 = us.f_main;
+    Params t = make_params(m, us.f_tail, sp.h + c0, f);
+    add_split_segs(t, sp.xh, sp.xl, k, sp.gh + c0, sp.gl + c0, f, k, sp.uh + c0, sp.ul + c0);
+    if (int rc = launch_n<128, 128, 2, true, Epi::kSwiGLUF32, 3>(t, 1, st, "swiglu_f32(up/gate tail)"))
+      return rc;
+  }
   if (int rc = split(sp.h, m * f, sp.hh, sp.hl, st, what)) return rc;
   if (int rc = split(w_down, f * k, sp.dh, sp.dl, st, what)) return rc;
   // Down GEMM [M,F]@[F,K]: with fewer 256x128 tiles than half the device

@@ -59,7 +59,8 @@ SMALL = {
     "add_rmsnorm_matmul": [dict(M=256, K=128, N=256), dict(M=50, K=96, N=72), dict(M=5, K=2048, N=40),
                            dict(M=33, K=2560, N=64)],
     "matmul_add_rmsnorm": [dict(M=256, K=128, N=256), dict(M=50, K=96, N=200), dict(M=300, K=64, N=520)],
-    "swiglu": [dict(M=256, K=64, N=128), dict(M=50, K=96, N=160)],
+    # F = 38400: 300 tiles of 256x128 on 256 CUs, the last 44 x 128 columns as 128x128 tiles
+    "swiglu": [dict(M=256, K=64, N=128), dict(M=50, K=96, N=160), dict(M=256, K=64, N=38400)],
 }
 
 
