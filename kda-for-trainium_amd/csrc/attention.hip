@@ -35,9 +35,13 @@
 //   that cross the causal diagonal or the sequence end.
 //   Software pipeline, per iteration kt: the MFMAs of O += V(kt-1) P(kt-1) run in
 //   one basic block with the row-max test of S(kt); after the (rarely taken)
-//   running-max update, the MFMAs of S(kt+1) = K(kt+1) Q^T run in one basic
-//   block with the exponentials of S(kt).  A wave's MFMAs execute while it
-//   issues its VALU work.
+//   running-max update, the exponentials of S(kt) and the MFMAs of
+//   S(kt+1) = K(kt+1) Q^T run in a second block, S(kt+1) accumulating into the
+//   registers of S(kt) tile by tile.  The K and V fragments are read kAhead
+//   fragments ahead of the MFMAs that use them, pinned in program order, so
+//   several LDS reads are in flight per wave.  The second wave of each SIMD
+//   runs at a raised issue priority so both reach the per-iteration barrier
+//   together.
 #include "common.h"
 #include "lanes.h"
 #include "lds_dma.h"
