@@ -65,12 +65,22 @@ class Timing:
     p90_ms: float
     mean_ms: float
     samples: int
+    # Mean time per call over one uninterrupted run of `samples` back-to-back
+    # calls between two events: the per-call launch duration without the
+    # event-to-dispatch latency that each single-call sample includes.
+    region_ms: Optional[float] = None
 
 
 def time_op(fn: Callable[[int], Any], warmup: int = 20, iters: int = 100,
             device: Optional[torch.device] = None, min_warmup_s: float = 0.2,
-            max_warmup: int = 4000) -> Timing:
+            max_warmup: int = 4000, region_reps: int = 0) -> Timing:
     """Times ``fn(i)`` with HIP events on the current stream; returns p50/p10/p90.
+
+    Each of the ``iters`` samples brackets one call with its own pair of events.
+    With ``region_reps`` > 0, a further ``region_reps`` calls run back to back
+    between a single pair of events and ``region_ms`` is their mean: the
+    operator's launch duration as a kernel profiler reports it, without the few
+    microseconds between a start event and the first wave of the call.
 
     ``fn`` receives the iteration index so a caller can rotate through several
     input sets (memory-bound operators rotate more than the 256 MB Infinity
@@ -100,8 +110,18 @@ def time_op(fn: Callable[[int], Any], warmup: int = 20, iters: int = 100,
     torch.cuda.synchronize(dev)
     ms = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
     q = lambda f: ms[min(len(ms) - 1, int(f * (len(ms) - 1) + 0.5))]
+    region = None
+    if region_reps:
+        r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        base = done + iters
+        r0.record(stream)
+        for i in range(region_reps):
+            fn(base + i)
+        r1.record(stream)
+        torch.cuda.synchronize(dev)
+        region = r0.elapsed_time(r1) / region_reps
     return Timing(p50_ms=statistics.median(ms), p10_ms=q(0.1), p90_ms=q(0.9),
-                  mean_ms=sum(ms) / len(ms), samples=len(ms))
+                  mean_ms=sum(ms) / len(ms), samples=len(ms), region_ms=region)
 
 
 def roofline(work: float, seconds: float, bound: str) -> Dict[str, Any]:

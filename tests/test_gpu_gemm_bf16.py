@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from gpu_util import SEEDS, to_dev, to_host
-from kda import ops
+from kda import _lib, ops
 from oracle import inputs as oi
 from oracle import ops as oo
 from oracle.numerics import rel_l2, to_bf16_rne
@@ -170,6 +170,25 @@ def test_swiglu_config_without_split_k_workspace(dev):
         assert err < BF16_GATE
     # the two orders of the F sum differ by at most one bf16 rounding of the output
     assert rel_l2(got, split) < 2.0 ** -8
+
+
+def test_swiglu_split_k_ragged_rows_dirty_workspace(dev):
+    # M = 300 (a ragged second row of 256-row tiles), F = 17408: 272 gate/up tiles,
+    # so on 256 CUs the last 1024 columns run as a round of 128x128 tiles; the
+    # down GEMM's 14 tiles run with F split in two into fp32 partials.  The
+    # workspace starts as 0xff bytes (nothing in it may be read before it is
+    # written), and a second call on the same workspace gives the same bits.
+    m, k, f = 300, 1792, 17408
+    d = oi.draw("swiglu_cfg", 3, dims=dict(M=m, K=k, F=f))
+    args = [to_dev(d[n], dev, BF) for n in ("x", "w_up", "w_down", "w_gate")]
+    ws = torch.full((ops.workspace_size(_lib.OP_SWIGLU_BF16, 1, m, k, f),), 255,
+                    dtype=torch.uint8, device=dev)
+    first = ops.swiglu(*args, workspace=ws)
+    second = ops.swiglu(*args, workspace=ws)
+    err = rel_l2(to_host(first), oo.swiglu(**d))
+    print(f"swiglu split-K M={m} K={k} F={f} rel_l2={err:.3e}", flush=True)
+    assert err < 5e-3
+    assert torch.equal(first, second)
 
 
 @pytest.mark.parametrize("dims", [dict(M=256, K=128, F=64), dict(M=50, K=96, F=200),
