@@ -1350,8 +1350,14 @@ extern "C" int kda_swiglu_bf16(const kda_bf16* x, const kda_bf16* w_up, const kd
   if (us.f_tail > 0) {
     Params t = make_params(m, us.f_tail, h + us.f_main, f);
     add_seg(t, x, k, w_gate + us.f_main, f, k, w_up + us.f_main);
-    if (int rc = launch<128, 128, 2, true, Epi::kSwiGLU>(t, 1, st, "swiglu_bf16(up/gate tail)"))
+    // 64-deep k-tiles in 3 slots (144 KiB): half the barriers per k of the 32-deep ring
+    // (measured 0.6 % faster for the operator; 2 slots were 2 % slower)
+    if (segments_fit(t, 64)) {
+      if (int rc = launch<128, 128, 2, true, Epi::kSwiGLU, 64, 3>(t, 1, st, "swiglu_bf16(up/gate tail)"))
+        return rc;
+    } else if (int rc = launch<128, 128, 2, true, Epi::kSwiGLU>(t, 1, st, "swiglu_bf16(up/gate tail)")) {
       return rc;
+    }
   }
   // Down GEMM y[M,K] = h[M,F] @ w_down[F,K].  When its 256x256 tiles fill at most
   // half the device (M = 2048, K = 4096: 128 tiles), F is split in two halves that
