@@ -579,19 +579,43 @@ __global__ __launch_bounds__(kSkThreads, 4) void bmm_smallk_kernel(const float* 
 
 // ---------------------------------------------------------------- pre-passes
 
-// fp32 -> (hi, lo) bf16 planes: hi = bf16(x), lo = bf16(x - hi), round to
-// nearest even.  Four elements per thread per step, grid-stride.
-__global__ __launch_bounds__(256) void split_f32_kernel(const floatx4* __restrict__ x,
-                                                        u32x2* __restrict__ hi, u32x2* __restrict__ lo,
-                                                        int64_t n4) {
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
-    const floatx4 v = __builtin_nontemporal_load(x + i);
-    uint32_t h0, h1, l0, l1;
-    split_bf16x2(v[0], v[1], h0, l0);
-    split_bf16x2(v[2], v[3], h1, l1);
-    hi[i] = u32x2{h0, h1};
-    lo[i] = u32x2{l0, l1};
+// Up to kMaxSplitJobs fp32 arrays, each split into (hi, lo) bf16 planes in one
+// launch: job t covers flat 4-element indices [end[t-1], end[t]).
+constexpr int kMaxSplitJobs = 4;
+struct SplitJobs {
+  const floatx4* x[kMaxSplitJobs];
+  u32x2* hi[kMaxSplitJobs];
+  u32x2* lo[kMaxSplitJobs];
+  int64_t end[kMaxSplitJobs];   // cumulative counts of 4-element groups
+  int n;
+};
+
+// One 4-element group of job-relative index i into its planes.
+__device__ __forceinline__ void split_group(const floatx4* __restrict__ x, u32x2* __restrict__ hi,
+                                            u32x2* __restrict__ lo, int64_t i) {
+  const floatx4 v = __builtin_nontemporal_load(x + i);
+  uint32_t h0, h1, l0, l1;
+  split_bf16x2(v[0], v[1], h0, l0);
+  split_bf16x2(v[2], v[3], h1, l1);
+  hi[i] = u32x2{h0, h1};
+  lo[i] = u32x2{l0, l1};
+}
+
+// Grid-stride over the groups of all jobs, starting at workgroup `b0` of `nb`.
+__device__ __forceinline__ void split_jobs(const SplitJobs& j, int64_t b0, int64_t nb) {
+  const int64_t total = j.end[j.n - 1];
+  for (int64_t i = b0 * 256 + threadIdx.x; i < total; i += nb * 256) {
+    int t = 0;
+#pragma unroll
+    for (int q = 0; q < kMaxSplitJobs - 1; ++q) t += (q < j.n - 1 && i >= j.end[q]) ? 1 : 0;
+    split_group(j.x[t], j.hi[t], j.lo[t], i - (t ? j.end[t - 1] : 0));
   }
+}
+
+// fp32 -> (hi, lo) bf16 planes: hi = bf16(x), lo = bf16(x - hi), round to
+// nearest even.  Four elements per thread per step, grid-stride over every job.
+__global__ __launch_bounds__(256) void split_f32_kernel(SplitJobs j) {
+  split_jobs(j, blockIdx.x, gridDim.x);
 }
 
 // Sum of S fp32 split-K partial planes [S][n] (in order of the planes), split
@@ -668,9 +692,15 @@ __global__ __launch_bounds__(256) void splitk2_f32_kernel(const floatx4* __restr
 // in the reference's operation order, and the result is split into (hi, lo)
 // bf16 planes for the GEMM.  K % 4 == 0.
 constexpr int kRowThreads = 256;
+// Workgroups past the last row split `w` (the GEMM's other operand) meanwhile.
+static_assert(kRowThreads == 256, "split_jobs assumes 256-thread workgroups");
 __global__ __launch_bounds__(kRowThreads) void rms_split_f32_kernel(
     const float* __restrict__ x, const float* __restrict__ z, const float* __restrict__ g,
-    uint16_t* __restrict__ hi, uint16_t* __restrict__ lo, int k, float eps) {
+    uint16_t* __restrict__ hi, uint16_t* __restrict__ lo, int k, float eps, int rows, SplitJobs w) {
+  if ((int)blockIdx.x >= rows) {
+    split_jobs(w, blockIdx.x - rows, gridDim.x - rows);
+    return;
+  }
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
   const int k4 = k / 4;
@@ -988,16 +1018,36 @@ int check_ws(const char* what, const void* ws, int64_t ws_bytes, int64_t need) {
   return KDA_OK;
 }
 
+// fp32 arrays to split into bf16 (hi, lo) planes by one launch.
+struct SplitBatch {
+  SplitJobs j{};
+  int add(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, const char* what) {
+    if (n % 4)
+      return set_error(KDA_ERR_UNSUPPORTED, "%s: element count %lld not a multiple of 4", what, (long long)n);
+    if (!aligned16(x)) return set_error(KDA_ERR_INVALID_ARG, "%s: fp32 input must be 16-byte aligned", what);
+    if (n == 0) return KDA_OK;
+    if (j.n == kMaxSplitJobs) return set_error(KDA_ERR_UNSUPPORTED, "%s: too many split jobs", what);
+    j.x[j.n] = reinterpret_cast<const floatx4*>(x);
+    j.hi[j.n] = reinterpret_cast<u32x2*>(hi);
+    j.lo[j.n] = reinterpret_cast<u32x2*>(lo);
+    j.end[j.n] = (j.n ? j.end[j.n - 1] : 0) + n / 4;
+    ++j.n;
+    return KDA_OK;
+  }
+  int64_t groups() const { return j.n ? j.end[j.n - 1] : 0; }
+  // workgroups of 256 threads for the batch (one group per thread, at most 16 per CU)
+  int64_t blocks() const { return std::min<int64_t>((groups() + 255) / 256, (int64_t)device_cu_count() * 16); }
+  int launch(hipStream_t st, const char* what) const {
+    if (groups() == 0) return KDA_OK;
+    hipLaunchKernelGGL(split_f32_kernel, dim3((unsigned)blocks()), dim3(256), 0, st, j);
+    return check_launch(what);
+  }
+};
+
 int split(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, hipStream_t st, const char* what) {
-  if (n % 4) return set_error(KDA_ERR_UNSUPPORTED, "%s: element count %lld not a multiple of 4", what, (long long)n);
-  if (!aligned16(x)) return set_error(KDA_ERR_INVALID_ARG, "%s: fp32 input must be 16-byte aligned", what);
-  const int64_t n4 = n / 4;
-  if (n4 == 0) return KDA_OK;
-  const int64_t blocks = std::min<int64_t>((n4 + 255) / 256, (int64_t)device_cu_count() * 16);
-  hipLaunchKernelGGL(split_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
-                     reinterpret_cast<const floatx4*>(x), reinterpret_cast<u32x2*>(hi),
-                     reinterpret_cast<u32x2*>(lo), n4);
-  return check_launch(what);
+  SplitBatch b;
+  if (int rc = b.add(x, n, hi, lo, what)) return rc;
+  return b.launch(st, what);
 }
 
 // ---- workspace plans (shared by the size query and the entry points)
@@ -1403,8 +1453,12 @@ extern "C" int kda_matmul_f32(const float* lhs, const float* rhs, float* out, in
   hipStream_t st = as_stream(stream);
   Carve cv{reinterpret_cast<uint8_t*>(workspace)};
   const SplitPlan s = plan_split(cv, m * k, k * n);
-  if (int rc = split(lhs, m * k, s.ah, s.al, st, what)) return rc;
-  if (int rc = split(rhs, k * n, s.bh, s.bl, st, what)) return rc;
+  {
+    SplitBatch sb;
+    if (int rc = sb.add(lhs, m * k, s.ah, s.al, what)) return rc;
+    if (int rc = sb.add(rhs, k * n, s.bh, s.bl, what)) return rc;
+    if (int rc = sb.launch(st, what)) return rc;
+  }
   Params p = make_params(m, n, out, n);
   add_split_segs(p, s.ah, s.al, k, s.bh, s.bl, n, k);
   return launch_auto<true, Epi::kStoreF32>(p, 1, st, what);
@@ -1467,8 +1521,12 @@ extern "C" int kda_bmm_f32(const float* lhs, const float* rhs, float* out, int64
     return rc;
   Carve cv{reinterpret_cast<uint8_t*>(workspace)};
   const SplitPlan s = plan_split(cv, batch * m * k, batch * k * n);
-  if (int rc = split(lhs, batch * m * k, s.ah, s.al, st, what)) return rc;
-  if (int rc = split(rhs, batch * k * n, s.bh, s.bl, st, what)) return rc;
+  {
+    SplitBatch sb;
+    if (int rc = sb.add(lhs, batch * m * k, s.ah, s.al, what)) return rc;
+    if (int rc = sb.add(rhs, batch * k * n, s.bh, s.bl, what)) return rc;
+    if (int rc = sb.launch(st, what)) return rc;
+  }
   Params p = make_params(m, n, out, n);
   add_split_segs(p, s.ah, s.al, k, s.bh, s.bl, n, k);
   p.batch_a = m * k;
@@ -1493,11 +1551,17 @@ extern "C" int kda_lora_f32(const float* x, const float* w, const float* a, cons
   hipStream_t st = as_stream(stream);
   Carve cv{reinterpret_cast<uint8_t*>(workspace)};
   const LoraPlan lp = plan_lora(cv, m, k, n, r);
-  if (int rc = split(x, m * k, lp.xw.ah, lp.xw.al, st, what)) return rc;
-  if (int rc = split(w, k * n, lp.xw.bh, lp.xw.bl, st, what)) return rc;
+  {
+    SplitBatch sb;
+    if (int rc = sb.add(x, m * k, lp.xw.ah, lp.xw.al, what)) return rc;
+    if (int rc = sb.add(w, k * n, lp.xw.bh, lp.xw.bl, what)) return rc;
+    if (r > 0) {
+      if (int rc = sb.add(a, k * r, lp.ah, lp.al, what)) return rc;
+      if (int rc = sb.add(b, r * n, lp.bh, lp.bl, what)) return rc;
+    }
+    if (int rc = sb.launch(st, what)) return rc;
+  }
   if (r > 0) {
-    if (int rc = split(a, k * r, lp.ah, lp.al, st, what)) return rc;
-    if (int rc = split(b, r * n, lp.bh, lp.bl, st, what)) return rc;
     // t = x @ a  [M, R]
     if (lp.parts > 1 && (m * r) % 4 == 0) {
       const int64_t kc = k / lp.parts;
@@ -1545,10 +1609,12 @@ static int rms_matmul_f32(const char* what, int op, const float* x, const float*
   hipStream_t st = as_stream(stream);
   Carve cv{reinterpret_cast<uint8_t*>(workspace)};
   const SplitPlan s = plan_split(cv, m * k, k * n);
-  hipLaunchKernelGGL(rms_split_f32_kernel, dim3((unsigned)m), dim3(kRowThreads), 0, st, x, z, g,
-                     s.ah, s.al, (int)k, eps);
+  // one launch: a workgroup per row of x, then the split of w
+  SplitBatch wb;
+  if (int rc = wb.add(w, k * n, s.bh, s.bl, what)) return rc;
+  hipLaunchKernelGGL(rms_split_f32_kernel, dim3((unsigned)(m + wb.blocks())), dim3(kRowThreads), 0, st,
+                     x, z, g, s.ah, s.al, (int)k, eps, (int)m, wb.j);
   if (int rc = check_launch(what)) return rc;
-  if (int rc = split(w, k * n, s.bh, s.bl, st, what)) return rc;
   Params p = make_params(m, n, out, n);
   add_split_segs(p, s.ah, s.al, k, s.bh, s.bl, n, k);
   return launch_auto<true, Epi::kStoreF32>(p, 1, st, what);
@@ -1592,8 +1658,12 @@ extern "C" int kda_matmul_add_rmsnorm_f32(const float* x, const float* w, float 
   Carve cv{reinterpret_cast<uint8_t*>(workspace)};
   const SplitPlan s = plan_split(cv, m * k, k * n);
   float* part = cv.take<float>(m * ((n + 31) / 32));
-  if (int rc = split(x, m * k, s.ah, s.al, st, what)) return rc;
-  if (int rc = split(w, k * n, s.bh, s.bl, st, what)) return rc;
+  {
+    SplitBatch sb;
+    if (int rc = sb.add(x, m * k, s.ah, s.al, what)) return rc;
+    if (int rc = sb.add(w, k * n, s.bh, s.bl, what)) return rc;
+    if (int rc = sb.launch(st, what)) return rc;
+  }
   Params p = make_params(m, n, out, n);
   add_split_segs(p, s.ah, s.al, k, s.bh, s.bl, n, k);
   p.z = z;
@@ -1631,9 +1701,13 @@ extern "C" int kda_swiglu_f32(const float* x, const float* w_up, const float* w_
   hipStream_t st = as_stream(stream);
   Carve cv{reinterpret_cast<uint8_t*>(workspace)};
   const SwigluPlan sp = plan_swiglu(cv, m, k, f);
-  if (int rc = split(x, m * k, sp.xh, sp.xl, st, what)) return rc;
-  if (int rc = split(w_gate, k * f, sp.gh, sp.gl, st, what)) return rc;
-  if (int rc = split(w_up, k * f, sp.uh, sp.ul, st, what)) return rc;
+  {
+    SplitBatch sb;
+    if (int rc = sb.add(x, m * k, sp.xh, sp.xl, what)) return rc;
+    if (int rc = sb.add(w_gate, k * f, sp.gh, sp.gl, what)) return rc;
+    if (int rc = sb.add(w_up, k * f, sp.uh, sp.ul, what)) return rc;
+    if (int rc = sb.launch(st, what)) return rc;
+  }
   // Gate/up GEMM: as on the bf16 path, columns that would leave the last round
   // of 256x128 tiles partly idle (4096 x 3072: 384 tiles, 1.5 rounds on 256 CUs)
   // run as one round of 128x128 dual-B tiles.
@@ -1648,8 +1722,12 @@ extern "C" int kda_swiglu_f32(const float* x, const float* w_up, const float* w_
     if (int rc = launch_n<128, 128, 2, true, Epi::kSwiGLUF32, 3>(t, 1, st, "swiglu_f32(up/gate tail)"))
       return rc;
   }
-  if (int rc = split(sp.h, m * f, sp.hh, sp.hl, st, what)) return rc;
-  if (int rc = split(w_down, f * k, sp.dh, sp.dl, st, what)) return rc;
+  {
+    SplitBatch sb;
+    if (int rc = sb.add(sp.h, m * f, sp.hh, sp.hl, what)) return rc;
+    if (int rc = sb.add(w_down, f * k, sp.dh, sp.dl, what)) return rc;
+    if (int rc = sb.launch(st, what)) return rc;
+  }
   // Down GEMM [M,F]@[F,K]: with fewer 256x128 tiles than half the device
   // (4096x1024: 128 tiles), F splits in two halves of every product segment,
   // run as a batch of two into fp32 partials and summed.
