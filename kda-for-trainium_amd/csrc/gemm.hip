@@ -75,7 +75,7 @@ enum class Epi {
   kRowScale,       // bf16 C = acc * row_scale[m]
   kSwiGLU,         // bf16 H = silu(acc_gate) * acc_up
   kStoreF32,       // fp32 C
-  kSwiGLUF32,      // fp32 H = silu(acc_gate) * acc_up
+  kSwiGLUSplit,    // h = silu(acc_gate) * acc_up in fp32, stored as its bf16 planes: hi = bf16(h) in C, lo = bf16(h - hi) in C2
   kAddZSsqF32,     // fp32 C = acc + z; part[m][n/64] = sum over the 64 columns of C^2
   kAddZSsqBf16,    // bf16 C = acc + z (bf16 z); part as above, from the fp32 sums
 };
@@ -93,6 +93,7 @@ struct Params {
   Seg seg[kMaxSeg];
   int nseg;
   void* c;                 // c[m*ldc + n]  (bf16, or fp32 for the *F32 epilogues)
+  void* c2;                // c2[m*ldc + n] bf16: the low plane (kSwiGLUSplit)
   const float* row_scale;  // [M]                      (kRowScale)
   const void* z;           // z[m*ldc + n], fp32 or bf16 as C   (kAddZSsq*)
   float* part;             // part[m*(N/WN) + n/WN]             (kAddZSsq*)
@@ -443,7 +444,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(Params p) {
         float v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          if constexpr (EPI == Epi::kSwiGLU || EPI == Epi::kSwiGLUF32)
+          if constexpr (EPI == Epi::kSwiGLU || EPI == Epi::kSwiGLUSplit)
             v[r] = silu_f(acc[0][i][j][r]) * acc[NB - 1][i][j][r];
           else
             v[r] = acc[0][i][j][r] * scale;
@@ -457,9 +458,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(Params p) {
           for (int r = 0; r < 4; ++r) ssq = fmaf(v[r], v[r], ssq);
         }
         const int64_t off = bz * p.batch_c + (int64_t)gm * p.ldc + gn;
-        if constexpr (EPI == Epi::kStoreF32 || EPI == Epi::kSwiGLUF32 || EPI == Epi::kAddZSsqF32) {
+        if constexpr (EPI == Epi::kStoreF32 || EPI == Epi::kAddZSsqF32) {
           *reinterpret_cast<floatx4*>(reinterpret_cast<float*>(p.c) + off) =
               floatx4{v[0], v[1], v[2], v[3]};
+        } else if constexpr (EPI == Epi::kSwiGLUSplit) {
+          uint32_t h0, h1, l0, l1;
+          split_bf16x2(v[0], v[1], h0, l0);
+          split_bf16x2(v[2], v[3], h1, l1);
+          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.c) + off) = u32x2{h0, h1};
+          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.c2) + off) = u32x2{l0, l1};
         } else {
           *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.c) + off) =
               u32x2{pack2(v[0], v[1]), pack2(v[2], v[3])};
@@ -1099,7 +1106,6 @@ LoraPlan plan_lora(Carve& c, int64_t m, int64_t k, int64_t n, int64_t r) {
 }
 struct SwigluPlan {
   uint16_t *xh, *xl, *gh, *gl, *uh, *ul;
-  float* h;
   uint16_t *hh, *hl, *dh, *dl;
   float* part;
 };
@@ -1111,7 +1117,6 @@ SwigluPlan plan_swiglu(Carve& c, int64_t m, int64_t k, int64_t f) {
   p.gl = c.take<uint16_t>(k * f);
   p.uh = c.take<uint16_t>(k * f);
   p.ul = c.take<uint16_t>(k * f);
-  p.h = c.take<float>(m * f);
   p.hh = c.take<uint16_t>(m * f);
   p.hl = c.take<uint16_t>(m * f);
   p.dh = c.take<uint16_t>(f * k);
@@ -1706,27 +1711,25 @@ extern "C" int kda_swiglu_f32(const float* x, const float* w_up, const float* w_
     if (int rc = sb.add(x, m * k, sp.xh, sp.xl, what)) return rc;
     if (int rc = sb.add(w_gate, k * f, sp.gh, sp.gl, what)) return rc;
     if (int rc = sb.add(w_up, k * f, sp.uh, sp.ul, what)) return rc;
+    if (int rc = sb.add(w_down, f * k, sp.dh, sp.dl, what)) return rc;
     if (int rc = sb.launch(st, what)) return rc;
   }
   // Gate/up GEMM: as on the bf16 path, columns that would leave the last round
   // of 256x128 tiles partly idle (4096 x 3072: 384 tiles, 1.5 rounds on 256 CUs)
-  // run as one round of 128x128 dual-B tiles.
+  // run as one round of 128x128 dual-B tiles.  The epilogue stores h =
+  // silu(g) * u (fp32) directly as the bf16 (hi, lo) planes the down GEMM reads.
   const UpSplit us = plan_up(m, f);
-  Params up = make_params(m, us.f_main, sp.h, f);
+  Params up = make_params(m, us.f_main, sp.hh, f);
+  up.c2 = sp.hl;
   add_split_segs(up, sp.xh, sp.xl, k, sp.gh, sp.gl, f, k, sp.uh, sp.ul);
-  if (int rc = launch<256, 128, 2, true, Epi::kSwiGLUF32>(up, 1, st, "swiglu_f32(up/gate)")) return rc;
+  if (int rc = launch<256, 128, 2, true, Epi::kSwiGLUSplit>(up, 1, st, "swiglu_f32(up/gate)")) return rc;
   if (us.f_tail > 0) {
     const int64_t c0 = us.f_main;
-    Params t = make_params(m, us.f_tail, sp.h + c0, f);
+    Params t = make_params(m, us.f_tail, sp.hh + c0, f);
+    t.c2 = sp.hl + c0;
     add_split_segs(t, sp.xh, sp.xl, k, sp.gh + c0, sp.gl + c0, f, k, sp.uh + c0, sp.ul + c0);
-    if (int rc = launch_n<128, 128, 2, true, Epi::kSwiGLUF32, 3>(t, 1, st, "swiglu_f32(up/gate tail)"))
+    if (int rc = launch_n<128, 128, 2, true, Epi::kSwiGLUSplit, 3>(t, 1, st, "swiglu_f32(up/gate tail)"))
       return rc;
-  }
-  {
-    SplitBatch sb;
-    if (int rc = sb.add(sp.h, m * f, sp.hh, sp.hl, what)) return rc;
-    if (int rc = sb.add(w_down, f * k, sp.dh, sp.dl, what)) return rc;
-    if (int rc = sb.launch(st, what)) return rc;
   }
   // Down GEMM [M,F]@[F,K]: with fewer 256x128 tiles than half the device
   // (4096x1024: 128 tiles), F splits in two halves of every product segment,
