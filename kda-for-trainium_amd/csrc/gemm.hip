@@ -644,10 +644,18 @@ __global__ __launch_bounds__(256) void sum_split_f32_kernel(const floatx4* __res
 // x [K][M] fp32 -> bf16 hi/lo planes of x^T, [M][K] (K-contiguous, so the GEMM
 // reads A with ds_read_b128 fragments instead of transposed LDS reads).  One
 // workgroup per 64 x 64 block through LDS; M % 8 == 0, K % 8 == 0.
+// Rows of workgroups at blockIdx.y >= kblocks split `w` (the GEMM's B operand)
+// meanwhile.
 __global__ __launch_bounds__(256) void split_transpose_f32_kernel(const float* __restrict__ x,
                                                                   uint16_t* __restrict__ hi,
                                                                   uint16_t* __restrict__ lo,
-                                                                  int64_t k, int64_t m) {
+                                                                  int64_t k, int64_t m, int kblocks,
+                                                                  SplitJobs w) {
+  if ((int)blockIdx.y >= kblocks) {
+    split_jobs(w, (int64_t)(blockIdx.y - kblocks) * gridDim.x + blockIdx.x,
+               (int64_t)(gridDim.y - kblocks) * gridDim.x);
+    return;
+  }
   __shared__ float tile[64][65];
   const int64_t m0 = (int64_t)blockIdx.x * 64, k0 = (int64_t)blockIdx.y * 64;
   for (int i = threadIdx.x; i < 64 * 16; i += 256) {
@@ -1489,11 +1497,15 @@ extern "C" int kda_transpose_matmul_f32(const float* lhs, const float* rhs, floa
   // lhs [K][M] is split and transposed in one pass, so the GEMM runs on
   // K-contiguous A planes (measured faster than transposed LDS reads of [K][M])
   if (!aligned16(lhs)) return set_error(KDA_ERR_INVALID_ARG, "%s: lhs must be 16-byte aligned", what);
-  if ((k + 63) / 64 > 65535) return set_error(KDA_ERR_UNSUPPORTED, "%s: K too large", what);
-  hipLaunchKernelGGL(split_transpose_f32_kernel, dim3((unsigned)((m + 63) / 64), (unsigned)((k + 63) / 64)),
-                     dim3(256), 0, st, lhs, s.ah, s.al, k, m);
+  // one launch: the 64x64 blocks of lhs, then rows of workgroups that split rhs
+  SplitBatch wb;
+  if (int rc = wb.add(rhs, k * n, s.bh, s.bl, what)) return rc;
+  const int64_t mblocks = (m + 63) / 64, kblocks = (k + 63) / 64;
+  const int64_t wrows = (wb.blocks() + mblocks - 1) / mblocks;
+  if (kblocks + wrows > 65535) return set_error(KDA_ERR_UNSUPPORTED, "%s: K too large", what);
+  hipLaunchKernelGGL(split_transpose_f32_kernel, dim3((unsigned)mblocks, (unsigned)(kblocks + wrows)),
+                     dim3(256), 0, st, lhs, s.ah, s.al, k, m, (int)kblocks, wb.j);
   if (int rc = check_launch(what)) return rc;
-  if (int rc = split(rhs, k * n, s.bh, s.bl, st, what)) return rc;
   Params p = make_params(m, n, out, n);
   add_split_segs(p, s.ah, s.al, k, s.bh, s.bl, n, k);   // A planes [M][K]: lda = K
   return launch_auto<true, Epi::kStoreF32>(p, 1, st, what);
