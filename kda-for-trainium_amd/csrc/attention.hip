@@ -39,7 +39,9 @@
 //   S(kt+1) = K(kt+1) Q^T run in a second block, S(kt+1) accumulating into the
 //   registers of S(kt) tile by tile.  The K and V fragments are read kAhead
 //   fragments ahead of the MFMAs that use them, pinned in program order, so
-//   several LDS reads are in flight per wave.  The second wave of each SIMD
+//   several LDS reads are in flight per wave; the reads run on across the two
+//   blocks (the first block's last slots fetch the second's first K fragments).
+//   The second wave of each SIMD
 //   runs at a raised issue priority so both reach the per-iteration barrier
 //   together.
 #include "common.h"
@@ -146,6 +148,30 @@ __device__ __forceinline__ void accumulate_pv(State& st, const uint8_t* v_lds,
   }
 }
 
+// accumulate_pv whose last kAhead read slots fetch the first kAhead K fragments
+// of the block B that follows (K(kt+1) has landed since the previous barrier), so
+// the read stream runs on across the two blocks (0.5 % same-box).
+__device__ __forceinline__ void accumulate_pv_k(State& st, const uint8_t* v_lds,
+                                                const bf16x8 (&pf)[kIT][2], int lane,
+                                                const uint8_t* k_lds, bf16x8 (&kf0)[kAhead]) {
+  bf16x8 vf[16];
+#pragma unroll
+  for (int f = 0; f < kAhead; ++f) vf[f] = read_mn_frag<kD>(v_lds, (f & 7) * 16, 32 * (f >> 3), lane);
+  pin_reads();
+#pragma unroll
+  for (int f = 0; f < 16; ++f) {
+    if (f + kAhead < 16)
+      vf[f + kAhead] = read_mn_frag<kD>(v_lds, ((f + kAhead) & 7) * 16, 32 * ((f + kAhead) >> 3), lane);
+    else
+      kf0[f + kAhead - 16] = k_frag(k_lds, (f + kAhead - 16) >> 2, (f + kAhead - 16) & 3, lane);
+    pin_reads();
+    const int c = f >> 3, dt = f & 7;
+#pragma unroll
+    for (int it = 0; it < kIT; ++it)
+      st.o[it][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[f], pf[it][c], st.o[it][dt], 0, 0, 0);
+  }
+}
+
 // Online softmax of S(kt) (accumulators s = t - m in log2 units, t the scaled
 // score, m the row's running max), first half: masking and the row-max test.
 // Returns whether some row of the wave has a score above m + kLazy.  A row's max
@@ -240,13 +266,16 @@ __device__ __forceinline__ void softmax_probs(State& st, const floatx4 (&s)[kIT]
 // S(kt+1) = K(kt+1) Q^T - m, key tile by key tile in place: tile t's exps and
 // packs read s[.][t] before the MFMAs of S(kt+1) overwrite it, so S(kt+1) needs
 // no second set of accumulators.
+// PRE: the first kAhead K fragments are already in kf0 (read by accumulate_pv_k).
+template <bool PRE>
 __device__ __forceinline__ void probs_then_scores(State& st, const uint8_t* k_lds, int lane,
-                                                  floatx4 (&s)[kIT][4], bf16x8 (&pf)[kIT][2]) {
+                                                  floatx4 (&s)[kIT][4], bf16x8 (&pf)[kIT][2],
+                                                  const bf16x8 (&kf0)[kAhead]) {
   uint32_t w[kIT][2][4];
   // K fragments (t, dc) in order f = 4t + dc, read kAhead ahead of their MFMAs
   bf16x8 kf[16];
 #pragma unroll
-  for (int f = 0; f < kAhead; ++f) kf[f] = k_frag(k_lds, f >> 2, f & 3, lane);
+  for (int f = 0; f < kAhead; ++f) kf[f] = PRE ? kf0[f] : k_frag(k_lds, f >> 2, f & 3, lane);
   pin_reads();
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
@@ -405,6 +434,7 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   floatx4 s[kIT][4];
   bf16x8 pf[kIT][2];
   float alpha[kIT];
+  bf16x8 kf0[kAhead];   // first K fragments of the next block B, read at the end of block A
   scores(st, k_tile(0), lane, s);
   __syncthreads();
 
@@ -441,7 +471,7 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
     if (nfree > 0) softmax_test<CAUSAL, false>(p, 0, w0, lane, s, x);
     else softmax_test<CAUSAL, true>(p, 0, w0, lane, s, x);
     softmax_raise<true>(st, s, x, alpha);
-    if (nkt > 1) probs_then_scores(st, k_tile(1), lane, s, pf);
+    if (nkt > 1) probs_then_scores<false>(st, k_tile(1), lane, s, pf, kf0);
     else softmax_probs(st, s, pf);
     finish();
   }
@@ -453,19 +483,19 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   for (; kt < n_mid_free; ++kt) {
     fetch(kt);
     rescale(any);
-    accumulate_pv(st, v_tile(kt - 1), pf, lane);
+    accumulate_pv_k(st, v_tile(kt - 1), pf, lane, k_tile(kt + 1), kf0);
     any = softmax_test<CAUSAL, false>(p, kt, w0, lane, s, x);
     if (any) softmax_raise<false>(st, s, x, alpha);
-    probs_then_scores(st, k_tile(kt + 1), lane, s, pf);
+    probs_then_scores<true>(st, k_tile(kt + 1), lane, s, pf, kf0);
     finish();
   }
   for (; kt < nkt - 1; ++kt) {
     fetch(kt);
     rescale(any);
-    accumulate_pv(st, v_tile(kt - 1), pf, lane);
+    accumulate_pv_k(st, v_tile(kt - 1), pf, lane, k_tile(kt + 1), kf0);
     any = softmax_test<CAUSAL, true>(p, kt, w0, lane, s, x);
     if (any) softmax_raise<false>(st, s, x, alpha);
-    probs_then_scores(st, k_tile(kt + 1), lane, s, pf);
+    probs_then_scores<true>(st, k_tile(kt + 1), lane, s, pf, kf0);
     finish();
   }
   if (kt == nkt - 1 && kt >= 1) {   // last tile: no S(kt+1)
