@@ -43,7 +43,8 @@
 //
 // Tile order: workgroups are dealt round-robin to the 8 XCDs, so consecutive
 // tile ids are remapped onto one XCD (sharing its L2), then walked in groups of
-// kGroupM tile-rows so co-resident tiles reuse the same A rows and B columns.
+// group_m tile-rows (chosen per launch) so co-resident tiles reuse the same A
+// rows and B columns.
 #include <math.h>
 
 #include <mutex>
@@ -60,7 +61,6 @@ constexpr int kWaves = kWavesM * kWavesN;     // 8 waves: 2 per SIMD
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBK = 32;        // k per LDS slot
 constexpr int kStages = 4;     // LDS slots (4 x 32 KiB for a 256x256 tile)
-constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
 constexpr int kMaxSeg = 6;
 
@@ -100,6 +100,7 @@ struct Params {
   int64_t ldc;
   int64_t batch_a, batch_b, batch_c;   // per-batch strides (elements), batch = blockIdx.y
   int m, n, k;             // k = sum of segment extents
+  int group_m;             // tile rows per group of the tile order (set at launch)
 };
 
 // Position of 16-byte chunk c of row r in a K-contiguous tile of BK-element
@@ -110,15 +111,15 @@ template <int BK>
 __device__ __forceinline__ int kswz(int r) { return BK == 32 ? ((r >> 1) & 3) : (r & 7); }
 
 // Maps the linear workgroup id to (tile_m, tile_n): XCD-contiguous, grouped by rows.
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
   const int total = tiles_m * tiles_n;
   int pid = blockIdx.x;
   const int full = (total / kXcds) * kXcds;
   if (pid < full) pid = (pid % kXcds) * (full / kXcds) + pid / kXcds;
-  const int per_group = kGroupM * tiles_n;
+  const int per_group = group_m * tiles_n;
   const int group = pid / per_group;
-  const int first_m = group * kGroupM;
-  const int gsize = min(tiles_m - first_m, kGroupM);
+  const int first_m = group * group_m;
+  const int gsize = min(tiles_m - first_m, group_m);
   const int local = pid - group * per_group;
   tm = first_m + local % gsize;
   tn = local / gsize;
@@ -168,7 +169,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(Params p) {
 
   const int tiles_m = (p.m + BM - 1) / BM, tiles_n = (p.n + BN - 1) / BN;
   int tm, tn;
-  tile_coords(tiles_m, tiles_n, tm, tn);
+  tile_coords(tiles_m, tiles_n, p.group_m, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int M = p.m, N = p.n, K = p.k;
   const int nk = (K + BK - 1) / BK;
@@ -904,8 +905,35 @@ __global__ __launch_bounds__(kPrepThreads) void rms_prep_kernel(const uint16_t* 
 
 // ---------------------------------------------------------------- launch helpers
 
+// Tile-row group height of the tile order.  Every tile shape here holds one
+// workgroup per CU, so each XCD runs about T tiles at a time: a grid that fits
+// the device at once keeps all its batches resident, else the first CU-count
+// tiles of batch 0 are.  Per k-step those T tiles fetch g*BM rows of A and
+// ceil(T/g)*BN*NB columns of B into the XCD's L2; the g minimizing that sum is
+// taken, the larger on a tie.  (Split-K SwiGLU down GEMM, 8x16 tiles of 256x256
+// in 2 batches: T = 16, g = 4, measured 4 % faster than g = 8; the 256-tile
+// launches with T = 32 tie from g = 4 to 8 and measure alike.)
+int pick_group_m(int tiles_m, int tiles_n, int batch, int bm, int bn_all) {
+  const int64_t tiles = (int64_t)tiles_m * tiles_n;
+  const int64_t cus = device_cu_count();
+  const int64_t conc = tiles * batch <= cus ? tiles : std::min(tiles, cus);
+  const int t = (int)std::max<int64_t>(1, conc / kXcds);
+  int best = 1;
+  int64_t best_cost = INT64_MAX;
+  for (int g = 1; g <= std::min(tiles_m, t); ++g) {
+    const int64_t cost = (int64_t)g * bm + (int64_t)((t + g - 1) / g) * bn_all;
+    if (cost <= best_cost) {
+      best = g;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
 template <int BM, int BN, int NB, bool A_KMAJ, Epi EPI, int NSEG, int BK = kBK, int S = kStages>
-int launch_n(const Params& a, int batch, hipStream_t st, const char* what) {
+int launch_n(const Params& p, int batch, hipStream_t st, const char* what) {
+  Params a = p;
+  a.group_m = pick_group_m((a.m + BM - 1) / BM, (a.n + BN - 1) / BN, batch, BM, BN * NB);
   const int tiles = ((a.m + BM - 1) / BM) * ((a.n + BN - 1) / BN);
   const size_t lds = (size_t)S * (BM + NB * BN) * BK * sizeof(uint16_t);
   static const bool attr_ok = [&] {
