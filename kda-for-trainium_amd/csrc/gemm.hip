@@ -1768,7 +1768,11 @@ extern "C" int kda_swiglu_f32(const float* x, const float* w_up, const float* w_
     Params t = make_params(m, us.f_tail, sp.hh + c0, f);
     t.c2 = sp.hl + c0;
     add_split_segs(t, sp.xh, sp.xl, k, sp.gh + c0, sp.gl + c0, f, k, sp.uh + c0, sp.ul + c0);
-    if (int rc = launch_n<128, 128, 2, true, Epi::kSwiGLUSplit, 3>(t, 1, st, "swiglu_f32(up/gate tail)"))
+    // 64-deep k-tiles in 3 slots, as the bf16 tail
+    if (int rc = segments_fit(t, 64)
+                     ? launch_n<128, 128, 2, true, Epi::kSwiGLUSplit, 3, 64, 3>(t, 1, st,
+                                                                                "swiglu_f32(up/gate tail)")
+                     : launch_n<128, 128, 2, true, Epi::kSwiGLUSplit, 3>(t, 1, st, "swiglu_f32(up/gate tail)"))
       return rc;
   }
   // Down GEMM [M,F]@[F,K]: with fewer 256x128 tiles than half the device
