@@ -455,24 +455,19 @@ struct Plan {
 };
 Plan plan(void* ws, int64_t batch, int64_t seq, int64_t hq, int64_t hkv) {
   Plan pl;
-  uint8_t* base = reinterpret_cast<uint8_t*>(ws);
-  int64_t used = 0;
-  auto take = [&](int64_t bytes) {
-    const int64_t off = (used + 255) & ~int64_t(255);
-    used = off + bytes;
-    return base ? base + off : nullptr;
-  };
+  Carve c{reinterpret_cast<uint8_t*>(ws)};
   (void)hq;
-  const int64_t nk = batch * seq * hkv * kD;
-  const int64_t nt = (seq + kBN - 1) / kBN;
-  pl.k0 = reinterpret_cast<_Float16*>(take(nk * 2));
-  pl.k1 = reinterpret_cast<_Float16*>(take(nk * 2));
-  pl.v0 = reinterpret_cast<_Float16*>(take(nk * 2));
-  pl.v1 = reinterpret_cast<_Float16*>(take(nk * 2));
-  pl.kinv = reinterpret_cast<float*>(take(batch * hkv * nt * 4));
-  pl.vtmax = reinterpret_cast<float*>(take(batch * hkv * nt * 4));
-  pl.vinv = reinterpret_cast<float*>(take(batch * hkv * 4));
-  pl.bytes = used;
+  const SizeTerm nk = SizeTerm(batch) * seq * hkv * kD;   // elements per limb plane
+  const SizeTerm heads = SizeTerm(batch) * hkv;
+  const SizeTerm nt = ceil_div(seq, kBN);
+  pl.k0 = c.take<_Float16>(nk);
+  pl.k1 = c.take<_Float16>(nk);
+  pl.v0 = c.take<_Float16>(nk);
+  pl.v1 = c.take<_Float16>(nk);
+  pl.kinv = c.take<float>(heads * nt);
+  pl.vtmax = c.take<float>(heads * nt);
+  pl.vinv = c.take<float>(heads);
+  pl.bytes = c.used;   // -1 when the sizes have no representable workspace
   return pl;
 }
 
@@ -521,7 +516,7 @@ extern "C" int kda_gqa_fwd_f32(const float* q, const float* k, const float* v, f
       batch * seq * hq * kD * 2 > ((int64_t)1 << 32))
     return set_error(KDA_ERR_UNSUPPORTED, "%s: problem too large", what);
   const Plan pl = plan(workspace, batch, seq, hq, hkv);
-  if (!workspace || !aligned16(workspace) || workspace_bytes < pl.bytes)
+  if (pl.bytes < 0 || !workspace || !aligned16(workspace) || workspace_bytes < pl.bytes)
     return set_error(KDA_ERR_INVALID_ARG, "%s: workspace must be 16-byte aligned and >= %lld bytes",
                      what, (long long)pl.bytes);
   hipStream_t st = as_stream(stream);

@@ -435,7 +435,7 @@ extern "C" int kda_bmm_softmax_f32(const float* lhs, const float* rhs, float* ou
   if (!lhs || !rhs || !out) return set_error(KDA_ERR_INVALID_ARG, "%s: null pointer", what);
   if (!aligned16(out)) return set_error(KDA_ERR_INVALID_ARG, "%s: out must be 16-byte aligned", what);
   const int64_t need = kda_workspace_size(KDA_OP_BMM_SOFTMAX_F32, batch, m, k, n, 0);
-  if (!workspace || !aligned16(workspace) || ws_bytes < need)
+  if (need < 0 || !workspace || !aligned16(workspace) || ws_bytes < need)
     return set_error(KDA_ERR_INVALID_ARG, "%s: workspace must be 16-byte aligned and >= %lld bytes",
                      what, (long long)need);
   hipStream_t st = as_stream(stream);

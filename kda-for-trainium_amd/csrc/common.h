@@ -30,6 +30,48 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // Number of compute units on the current device (cached per device).
 int device_cu_count();
 
+// ---- workspace size arithmetic (host) ---------------------------------------
+// A size term built from caller-supplied sizes: products and sums of terms go
+// invalid (-1) on a negative operand or on int64 overflow instead of wrapping,
+// so a size query never overflows and never reports a buffer smaller than the
+// one the kernels would use.
+struct SizeTerm {
+  int64_t v;
+  constexpr SizeTerm(int64_t x) : v(x < 0 ? -1 : x) {}
+  bool ok() const { return v >= 0; }
+  friend SizeTerm operator*(SizeTerm a, SizeTerm b) {
+    int64_t r;
+    return (!a.ok() || !b.ok() || __builtin_mul_overflow(a.v, b.v, &r)) ? SizeTerm(-1) : SizeTerm(r);
+  }
+  friend SizeTerm operator+(SizeTerm a, SizeTerm b) {
+    int64_t r;
+    return (!a.ok() || !b.ok() || __builtin_add_overflow(a.v, b.v, &r)) ? SizeTerm(-1) : SizeTerm(r);
+  }
+};
+// ceil(n / d) for n >= 0, d > 0 without forming n + d - 1; -1 for n < 0
+inline SizeTerm ceil_div(int64_t n, int64_t d) { return n < 0 ? SizeTerm(-1) : SizeTerm(n / d + (n % d != 0)); }
+
+// Bump allocator over a caller's workspace (256-byte aligned pieces).  With
+// base == nullptr it only measures, so the size query and the entry points share
+// one layout.  `used` becomes -1, and every later piece null, once a piece's
+// size is invalid or the total overflows.
+struct Carve {
+  uint8_t* base;
+  int64_t used = 0;
+  template <class T>
+  T* take(SizeTerm count) {
+    const SizeTerm start = SizeTerm(used) + 255;
+    const SizeTerm bytes = count * SizeTerm((int64_t)sizeof(T));
+    if (!start.ok() || !bytes.ok()) {
+      used = -1;
+      return nullptr;
+    }
+    const int64_t off = start.v & ~int64_t(255);
+    used = (SizeTerm(off) + bytes).v;
+    return (base && used >= 0) ? reinterpret_cast<T*>(base + off) : nullptr;
+  }
+};
+
 // Workspace bytes of kda_gqa_fwd_f32 (layout owned by attention_f32.hip).
 int64_t gqa_f32_workspace_bytes(int64_t batch, int64_t seq, int64_t hq, int64_t hkv);
 

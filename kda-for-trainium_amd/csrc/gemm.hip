@@ -1040,20 +1040,11 @@ int validate(const char* what, const void* a, const void* b, const void* c, int6
   return KDA_OK;
 }
 
-// Bump allocator over the caller's workspace; with base == nullptr it only
-// measures, so the size query and the entry points share one layout.
-struct Carve {
-  uint8_t* base;
-  int64_t used = 0;
-  template <class T>
-  T* take(int64_t count) {
-    const int64_t off = (used + 255) & ~int64_t(255);
-    used = off + count * (int64_t)sizeof(T);
-    return base ? reinterpret_cast<T*>(base + off) : nullptr;
-  }
-};
-
+// `need` is the operator's workspace_bytes(): -1 when its sizes have no
+// representable workspace, which is refused like a missing buffer.
 int check_ws(const char* what, const void* ws, int64_t ws_bytes, int64_t need) {
+  if (need < 0)
+    return set_error(KDA_ERR_UNSUPPORTED, "%s: sizes beyond the workspace's addressable range", what);
   if (need > 0 && (!ws || !aligned16(ws) || ws_bytes < need))
     return set_error(KDA_ERR_INVALID_ARG,
                      "%s: workspace must be 16-byte aligned and >= %lld bytes (got %lld)", what,
@@ -1097,7 +1088,7 @@ int split(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, hipStream_t st,
 struct SplitPlan {     // hi/lo planes of A [count_a] and B [count_b]
   uint16_t *ah, *al, *bh, *bl;
 };
-SplitPlan plan_split(Carve& c, int64_t count_a, int64_t count_b) {
+SplitPlan plan_split(Carve& c, SizeTerm count_a, SizeTerm count_b) {
   SplitPlan s;
   s.ah = c.take<uint16_t>(count_a);
   s.al = c.take<uint16_t>(count_a);
@@ -1112,9 +1103,9 @@ SplitPlan plan_split(Carve& c, int64_t count_a, int64_t count_b) {
 // kLoraMaxParts partials, so its size does not.
 constexpr int kLoraMaxParts = 16;
 int lora_t_parts(int64_t m, int64_t k, int64_t r) {
-  const int64_t tiles = ((m + 255) / 256) * ((r + 127) / 128);
+  const SizeTerm tiles = ceil_div(m, 256) * ceil_div(r, 128);
   int parts = 1;
-  while (parts < kLoraMaxParts && tiles * parts * 2 <= device_cu_count() &&
+  while (parts < kLoraMaxParts && tiles.ok() && tiles.v * parts * 2 <= device_cu_count() &&
          k % (parts * 2 * 64) == 0)
     parts *= 2;
   return parts;
@@ -1129,15 +1120,16 @@ struct LoraPlan {
 };
 LoraPlan plan_lora(Carve& c, int64_t m, int64_t k, int64_t n, int64_t r) {
   LoraPlan p;
-  p.xw = plan_split(c, m * k, k * n);
-  p.ah = c.take<uint16_t>(k * r);
-  p.al = c.take<uint16_t>(k * r);
+  const SizeTerm M(m), K(k), N(n), R(r);
+  p.xw = plan_split(c, M * K, K * N);
+  p.ah = c.take<uint16_t>(K * R);
+  p.al = c.take<uint16_t>(K * R);
   p.parts = r > 0 ? lora_t_parts(m, k, r) : 1;
-  p.t = c.take<float>(kLoraMaxParts * m * r);
-  p.th = c.take<uint16_t>(m * r);
-  p.tl = c.take<uint16_t>(m * r);
-  p.bh = c.take<uint16_t>(r * n);
-  p.bl = c.take<uint16_t>(r * n);
+  p.t = c.take<float>(SizeTerm(kLoraMaxParts) * M * R);
+  p.th = c.take<uint16_t>(M * R);
+  p.tl = c.take<uint16_t>(M * R);
+  p.bh = c.take<uint16_t>(R * N);
+  p.bl = c.take<uint16_t>(R * N);
   return p;
 }
 struct SwigluPlan {
@@ -1147,17 +1139,18 @@ struct SwigluPlan {
 };
 SwigluPlan plan_swiglu(Carve& c, int64_t m, int64_t k, int64_t f) {
   SwigluPlan p;
-  p.xh = c.take<uint16_t>(m * k);
-  p.xl = c.take<uint16_t>(m * k);
-  p.gh = c.take<uint16_t>(k * f);
-  p.gl = c.take<uint16_t>(k * f);
-  p.uh = c.take<uint16_t>(k * f);
-  p.ul = c.take<uint16_t>(k * f);
-  p.hh = c.take<uint16_t>(m * f);
-  p.hl = c.take<uint16_t>(m * f);
-  p.dh = c.take<uint16_t>(f * k);
-  p.dl = c.take<uint16_t>(f * k);
-  p.part = c.take<float>(2 * m * k);   // split-K partials of the down GEMM
+  const SizeTerm M(m), K(k), F(f);
+  p.xh = c.take<uint16_t>(M * K);
+  p.xl = c.take<uint16_t>(M * K);
+  p.gh = c.take<uint16_t>(K * F);
+  p.gl = c.take<uint16_t>(K * F);
+  p.uh = c.take<uint16_t>(K * F);
+  p.ul = c.take<uint16_t>(K * F);
+  p.hh = c.take<uint16_t>(M * F);
+  p.hl = c.take<uint16_t>(M * F);
+  p.dh = c.take<uint16_t>(F * K);
+  p.dl = c.take<uint16_t>(F * K);
+  p.part = c.take<float>(SizeTerm(2) * M * K);   // split-K partials of the down GEMM
   return p;
 }
 struct RmsBf16Plan {
@@ -1166,7 +1159,7 @@ struct RmsBf16Plan {
 };
 RmsBf16Plan plan_rms_bf16(Carve& c, int64_t m, int64_t k) {
   RmsBf16Plan p;
-  p.xg = c.take<uint16_t>(m * k);
+  p.xg = c.take<uint16_t>(SizeTerm(m) * k);
   p.inv = c.take<float>(m);
   return p;
 }
@@ -1189,34 +1182,24 @@ UpSplit plan_up(int64_t m, int64_t f) {
 }
 
 int64_t workspace_bytes(int op, int64_t b, int64_t m, int64_t k, int64_t n, int64_t r) {
-  // Every size term below is a product of at most three of the arguments times a
-  // small constant.  Sizes whose three largest arguments multiply to more than
-  // 2^40 elements (terabytes: beyond any device) have no workspace; below that no
-  // product or sum here can overflow.
+  // Every term is checked arithmetic (SizeTerm): sizes whose workspace does not
+  // fit in int64 give -1, as do negative sizes and unknown operators.
   if (b < 0 || m < 0 || k < 0 || n < 0 || r < 0) return -1;
-  {
-    double top[3] = {1.0, 1.0, 1.0};
-    for (const int64_t d : {b, m, k, n, r}) {
-      double v = d < 1 ? 1.0 : (double)d;
-      for (int i = 0; i < 3; ++i)
-        if (v > top[i]) { const double t = top[i]; top[i] = v; v = t; }
-    }
-    if (top[0] * top[1] * top[2] > (double)(int64_t(1) << 40)) return -1;
-  }
+  const SizeTerm B(b), M(m), K(k), N(n);
   Carve c{nullptr};
   switch (op) {
     case KDA_OP_MATMUL_F32:
     case KDA_OP_TRANSPOSE_MATMUL_F32:
     case KDA_OP_RMSNORM_MATMUL_F32:
     case KDA_OP_ADD_RMSNORM_MATMUL_F32:
-      plan_split(c, m * k, k * n);
+      plan_split(c, M * K, K * N);
       break;
     case KDA_OP_MATMUL_ADD_RMSNORM_F32:
-      plan_split(c, m * k, k * n);
-      c.take<float>(m * ((n + 31) / 32));
+      plan_split(c, M * K, K * N);
+      c.take<float>(M * ceil_div(n, 32));
       break;
     case KDA_OP_BMM_F32:
-      plan_split(c, b * m * k, b * k * n);
+      plan_split(c, B * M * K, B * K * N);
       break;
     case KDA_OP_LORA_F32:
       plan_lora(c, m, k, n, r);
@@ -1229,15 +1212,15 @@ int64_t workspace_bytes(int op, int64_t b, int64_t m, int64_t k, int64_t n, int6
       plan_rms_bf16(c, m, k);
       break;
     case KDA_OP_MATMUL_ADD_RMSNORM_BF16:  // row partials of the sum of squares
-      c.take<float>(m * ((n + 31) / 32));
+      c.take<float>(M * ceil_div(n, 32));
       break;
     case KDA_OP_BMM_SOFTMAX_F32:   // two fp16 limb planes of rhs^T [B][N][64], tile scales [B][N/64]
-      c.take<uint16_t>(2 * b * n * 64 + 2 * b * ((n + 63) / 64));
+      c.take<uint16_t>(SizeTerm(2) * B * N * 64 + SizeTerm(2) * B * ceil_div(n, 64));
       break;
     case KDA_OP_GQA_F32:           // m = S, k = Hq, n = Hkv
       return gqa_f32_workspace_bytes(b, m, k, n);
     case KDA_OP_SWIGLU_BF16:       // fp32 split-K partials of the down GEMM, [2][M][K]
-      c.take<float>(2 * m * k);
+      c.take<float>(SizeTerm(2) * M * K);
       break;
     default:
       return -1;
@@ -1401,16 +1384,21 @@ extern "C" int kda_rmsnorm_matmul_bf16_noalloc(const kda_bf16* x, const kda_bf16
                                                int64_t k, int64_t n, float eps, void* stream) {
   clear_error();
   const char* what = "rmsnorm_matmul_bf16_noalloc";
+  if (m < 0 || k < 0 || n < 0)
+    return set_error(KDA_ERR_INVALID_ARG, "%s: negative size (M=%lld K=%lld N=%lld)", what,
+                     (long long)m, (long long)k, (long long)n);
+  // The workspace depends on M and K only (bf16 normalised rows and 1/rms per row).
   const int64_t need = workspace_bytes(KDA_OP_RMSNORM_MATMUL_BF16, 1, m, k, n, 0);
-  if (need > KDA_NOALLOC_SCRATCH_BYTES)
+  if (need < 0 || need > KDA_NOALLOC_SCRATCH_BYTES)
     return set_error(KDA_ERR_UNSUPPORTED,
                      "%s: M=%lld K=%lld needs %lld bytes of scratch; the static buffer holds %lld "
                      "(2*M*K + 4*M bytes must fit)",
                      what, (long long)m, (long long)k, (long long)need,
                      (long long)KDA_NOALLOC_SCRATCH_BYTES);
+  // The scratch address is resolved for every call, so the entry point below never
+  // sees a null workspace with a non-zero size.
   void* ws = nullptr;
-  if (need > 0)   // negative sizes are reported by the call below, before any launch
-    if (int rc = scratch_address(what, &ws)) return rc;
+  if (int rc = scratch_address(what, &ws)) return rc;
   return kda_rmsnorm_matmul_bf16(x, gamma, w, y, m, k, n, eps, ws, KDA_NOALLOC_SCRATCH_BYTES,
                                  stream);
 }
@@ -1428,8 +1416,8 @@ extern "C" int kda_swiglu_bf16(const kda_bf16* x, const kda_bf16* w_up, const kd
   if (f == 0) return hipMemsetAsync(y, 0, (size_t)m * k * 2, as_stream(stream)) == hipSuccess
                          ? KDA_OK : set_error(KDA_ERR_HIP, "swiglu_bf16: memset failed");
   hipStream_t st = as_stream(stream);
-  const bool have_ws = workspace && aligned16(workspace) &&
-                       workspace_bytes_ >= workspace_bytes(KDA_OP_SWIGLU_BF16, 1, m, k, f, 0);
+  const int64_t ws_need = workspace_bytes(KDA_OP_SWIGLU_BF16, 1, m, k, f, 0);
+  const bool have_ws = workspace && aligned16(workspace) && ws_need >= 0 && workspace_bytes_ >= ws_need;
   // Gate/up GEMM: the columns that would leave the last round over the device
   // partly idle (2048 x 14336: 896 tiles of 256x128 = 3.5 rounds on 256 CUs)
   // run as one round of 128x128 tiles (measured 618 -> 604 us for the operator,

@@ -67,8 +67,44 @@ def test_workspace_sizes_are_host_arithmetic():
     assert q(_lib.OP_MATMUL_ADD_RMSNORM_BF16, 1, 7, 4096, 40, 0) == 4 * 7 * 2
     assert q(99, 1, 1, 1, 1, 0) == -1
     assert q(_lib.OP_MATMUL_F32, 1, -1, 32, 32, 0) == -1
-    assert q(_lib.OP_MATMUL_F32, 1, 1 << 40, 1 << 40, 8, 0) == -1     # beyond any device: no overflow
+    assert q(_lib.OP_MATMUL_F32, 1, 1 << 40, 1 << 40, 8, 0) == -1     # overflows int64: no size
     assert q(_lib.OP_BMM_SOFTMAX_F32, 1 << 30, 0, 64, 1 << 30, 0) == -1
+    assert q(_lib.OP_GQA_F32, 1 << 40, 1 << 40, 8, 8, 0) == -1
+
+
+def _pad(x):
+    return (x + 255) // 256 * 256
+
+
+def test_workspace_sizes_of_large_real_shapes():
+    """Shapes whose three largest sizes multiply past 2^40 still have a workspace:
+    each size term is checked on its own, so only a term that overflows int64 gives -1."""
+    q = lambda *a: _lib.query("kda_workspace_size", *a)
+    m, k, n = 8192, 8192, 28672                                        # fp32 split planes: 2*(2MK + 2KN)
+    assert q(_lib.OP_MATMUL_F32, 1, m, k, n, 0) == 2 * _pad(2 * m * k) + 2 * 2 * k * n
+    assert q(_lib.OP_RMSNORM_MATMUL_BF16, 1, 4096, 4096, 128256, 0) == 2 * 4096 * 4096 + 4 * 4096
+    assert q(_lib.OP_RMSNORM_MATMUL_BF16, 1, 4096, 4096, 65544, 0) == 2 * 4096 * 4096 + 4 * 4096
+    assert q(_lib.OP_SWIGLU_BF16, 1, 8192, 8192, 1 << 20, 0) == 8 * 8192 * 8192
+    assert q(_lib.OP_MATMUL_ADD_RMSNORM_BF16, 1, 1 << 20, 4096, 1 << 20, 0) == 4 * (1 << 20) * (1 << 15)
+    assert q(_lib.OP_GQA_F32, 64, 1 << 20, 32, 8, 0) > 4 * 2 * 64 * (1 << 20) * 8 * 128
+    # near the int64 limit: 8 * M * K bytes of partials
+    assert q(_lib.OP_SWIGLU_BF16, 1, 1, 1, 0, 0) == 8
+    assert q(_lib.OP_SWIGLU_BF16, 1, 1 << 30, 1 << 29, 8, 0) == 1 << 62
+    assert q(_lib.OP_SWIGLU_BF16, 1, 1 << 30, 1 << 30, 8, 0) == -1      # 2^63 bytes overflow
+
+
+def test_missing_workspace_refused_at_large_shapes():
+    """A null workspace is refused before any launch at sizes whose workspace is
+    large (no GPU is touched: the calls fail in argument validation)."""
+    fake = 1 << 20                                                      # aligned, never dereferenced
+    m, k, n = 8192, 8192, 28672
+    with pytest.raises(ValueError, match="workspace"):
+        _lib.call("kda_matmul_f32", fake, fake, fake, m, k, n, None, 0, None)
+    with pytest.raises(ValueError, match="workspace"):
+        _lib.call("kda_matmul_f32", fake, fake, fake, m, k, n, fake, 1 << 20, None)
+    with pytest.raises(ValueError, match="workspace"):
+        _lib.call("kda_rmsnorm_matmul_bf16", fake, fake, fake, fake, 4096, 4096, 128256, 1e-6,
+                  None, 0, None)
 
 
 def test_ops_reject_cpu_tensors():

@@ -59,6 +59,25 @@ for name, types in _lib.SIGNATURES.items():
         elif name != "kda_workspace_size" and not L.kda_last_error():
             bad += 1
             print(f"{name} case {case}: error without a message", flush=True)
+# Real shapes whose largest sizes multiply past 2^40 have positive workspace sizes,
+# and their entry points refuse a missing workspace before any launch.
+ws = L.kda_workspace_size
+ws.argtypes = _lib.SIGNATURES["kda_workspace_size"]
+ws.restype = ctypes.c_int64
+for op, dims in ((_lib.OP_MATMUL_F32, (1, 8192, 8192, 28672, 0)),
+                 (_lib.OP_RMSNORM_MATMUL_BF16, (1, 4096, 4096, 128256, 0)),
+                 (_lib.OP_RMSNORM_MATMUL_BF16, (1, 4096, 4096, 65544, 0))):
+    if ws(op, *dims) <= 0:
+        bad += 1
+        print(f"workspace size of op {op} at {dims}: {ws(op, *dims)}", flush=True)
+fake = 1 << 20
+for name, args in (("kda_matmul_f32", (fake, fake, fake, 8192, 8192, 28672, None, 0, None)),
+                   ("kda_rmsnorm_matmul_bf16", (fake, fake, fake, fake, 4096, 4096, 128256, 1e-6,
+                                                None, 0, None))):
+    f = getattr(L, name)
+    if f(*args) == 0:
+        bad += 1
+        print(f"{name} accepted a null workspace", flush=True)
 print(f"checked {len(_lib.SIGNATURES)} entry points, {bad} problems", flush=True)
 sys.exit(1 if bad else 0)
 """
