@@ -569,6 +569,12 @@ extern "C" int kda_gqa_fwd_bf16(const kda_bf16* q, const kda_bf16* k, const kda_
   const int64_t nblocks = ((seq + bm - 1) / bm) * batch * hkv * (group / hpw);
   if (nblocks > 0x7fffffff || seq > (1 << 30) || hq > (1 << 20))
     return set_error(KDA_ERR_UNSUPPORTED, "gqa_fwd_bf16: problem too large");
+  // The K/V DMAs address a tile's rows from a scalar base with 32-bit per-lane
+  // byte offsets (row * Hkv*D*2 + chunk, rows 0..63 of a tile).
+  if ((kBN - 1) * (hkv * kD * 2) + 2 * kD > (int64_t)0xffffffff)
+    return set_error(KDA_ERR_UNSUPPORTED,
+                     "gqa_fwd_bf16: Hkv=%lld kv heads exceed the 32-bit DMA offsets of a key tile",
+                     (long long)hkv);
 
   Args a;
   a.q = q;

@@ -107,6 +107,17 @@ def test_missing_workspace_refused_at_large_shapes():
                   None, 0, None)
 
 
+def test_gqa_bf16_rejects_kv_heads_beyond_32bit_dma_offsets():
+    """A key tile's 64 rows are addressed with 32-bit per-lane byte offsets
+    (row * Hkv*256 + chunk): Hkv = 266305 would wrap them, 266304 is the largest
+    that fits.  Refused before any launch (the pointers are never dereferenced)."""
+    fake = 1 << 20
+    for hkv in (266305, 1 << 20):
+        with pytest.raises(ValueError, match="32-bit DMA offsets"):
+            _lib.call("kda_gqa_fwd_bf16", fake, fake, fake, fake, 1, 64, hkv, hkv, 128, 0.088, 1,
+                      0, 0, 0, None)
+
+
 def test_ops_reject_cpu_tensors():
     import torch
     from kda import ops
