@@ -34,3 +34,22 @@ def threaded_heads(fn, heads, workers=8):
     from concurrent.futures import ThreadPoolExecutor
     with ThreadPoolExecutor(max_workers=workers) as pool:
         return np.stack(list(pool.map(fn, heads)))
+
+
+def batched_rel_l2(out, ref_fn, batches, workers=4):
+    """rel-L2 (float64 norms, as oracle.numerics.rel_l2) of a whole batched GPU
+    output against ref_fn(b) -> the oracle's batch b, accumulated batch by batch so
+    that only a few batches are on the host at once.  Returns (overall, per batch)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    def one(b):
+        got = out[b].detach().to(torch.float32).cpu().numpy().astype(np.float64)
+        want = np.asarray(ref_fn(b), dtype=np.float64).reshape(got.shape)
+        return float(np.sum((got - want) ** 2)), float(np.sum(want ** 2))
+
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        parts = list(pool.map(one, batches))
+    num = sum(p[0] for p in parts)
+    den = sum(p[1] for p in parts)
+    per = [float(np.sqrt(a / b)) if b else 0.0 for a, b in parts]
+    return float(np.sqrt(num / den)), per

@@ -3,12 +3,13 @@ vs the fp32 numpy oracle.  Gate: relative-L2 <= 1e-5 (stricter than the
 reference's 2e-5, adapter/nkibench_case.py:51).
 
 Full NKIBench shapes on the five seeds (different inputs per seed), plus small
-and ragged shapes.  bmm's 1 GB output is compared on two sampled batches."""
+and ragged shapes.  bmm's 1 GB output is compared whole on seed 0 and on three sampled
+batches for the other seeds."""
 import numpy as np
 import pytest
 import torch
 
-from gpu_util import SEEDS, to_dev, to_host
+from gpu_util import SEEDS, batched_rel_l2, to_dev, to_host
 from kda import ops
 from oracle import inputs as oi
 from oracle import ops as oo
@@ -83,6 +84,18 @@ def test_bmm_full_size_sampled_batches():
         assert err < GATE
         del out
         torch.cuda.empty_cache()
+
+
+def test_bmm_full_size_every_batch():
+    """Seed 0 at the NKIBench shape: all 16 batches of the 1.07 GB output."""
+    d = oi.draw("bmm", 0)
+    out = ops.bmm(to_dev(d["lhs"], "cuda"), to_dev(d["rhs"], "cuda"))
+    err, per = batched_rel_l2(out, lambda b: oo.bmm(d["lhs"][b:b + 1], d["rhs"][b:b + 1]),
+                              range(out.shape[0]))
+    print(f"bmm seed=0 all {out.shape[0]} batches rel_l2={err:.3e} worst batch {max(per):.3e}", flush=True)
+    assert out.shape[0] == 16 and err < GATE and max(per) < GATE
+    del out
+    torch.cuda.empty_cache()
 
 
 @pytest.mark.parametrize("dims", [dict(B=3, M=256, K=64, N=256), dict(B=2, M=100, K=96, N=72),
