@@ -3,7 +3,9 @@
     python -m kda.verify --op silu --case-module PATH [--fast] [--seeds 0,21,...]
     python -m kda.verify --op matmul --nkibench-root DIR [--case-id ID]
     python -m kda.verify --pilot | (no selector: every op of summary.json) --nkibench-root DIR
-    options: --baselines baselines.json  --ledger DIR  --json  --iters N  --warmup N  --rtol X
+    python -m kda.verify --build-baselines [--baselines baselines.json] <case selection>
+    options: --baselines baselines.json  --traffic FILE  --ledger DIR  --json  --iters N
+             --warmup N  --rtol X
 
 Follows the reference's evaluation contract (verify.py:13-65):
 - The golden is the case module's own numpy ``forward(...)``.  A case module is
@@ -24,8 +26,19 @@ Follows the reference's evaluation contract (verify.py:13-65):
   ``--baselines`` (the reference's baselines.json format) when one is given.
   Otherwise it is the case's numpy forward timed on this host, p50 of 3 after
   one warm-up.
+- ``--build-baselines`` measures each case's baseline (its numpy forward on this
+  host, p50 of 3 after one warm-up) and writes ``{"op[case=id]": {baseline_latency_ms,
+  case_id, kernel, op}}`` into the ``--baselines`` file (default baselines.json),
+  the format later runs read as their speedup denominator (verify.py:23,57-59).
+- ``summary_metrics`` holds the p10/p90 latency, the operator's bound (HBM or
+  MFMA), its achieved rate and fraction of the MI355X peak at the p50, and its
+  algorithmic HBM bytes (``kda.roofline``); with ``--traffic`` (the measured HBM
+  read/write bytes of a rocprofv3 profile at the same shapes) also those bytes.
+  Each op's line is followed by a one-line digest of them (verify.py:48-50,
+  README.md:146-147), which is also the ledger row's note.
 - One PASS/FAIL line per op, then the geomean of the speedups.  The exit code is
-  0 only if every scored op passed (verify.py:52-61).
+  0 only if every scored op passed, or with ``--build-baselines`` every baseline
+  was measured (verify.py:52-61).
 
 The library's callable for each op takes the forward() arguments in natural
 layout (kda.ops).  Keyword names are used when they match the callable's
@@ -149,14 +162,14 @@ def resolve_case(root: os.PathLike, op: str, case_id: Optional[str] = None,
     (adapter/nkibench_case.py:235-264); a single case is the default."""
     summary = load_summary(root)
     if op not in summary:
-        raise CaseError(f"operator {op!r} not in summary.json; have {sorted(summary)}")
+        raise CaseError(f"summary.json lists no operator {op!r} (it lists {', '.join(sorted(summary))})")
     cases = summary[op]["cases"]
     if case_id is None:
         if len(cases) != 1:
-            raise CaseError(f"{op} has cases {sorted(cases)}; pass --case-id")
+            raise CaseError(f"{op} lists {len(cases)} cases ({', '.join(sorted(cases))}): choose one with --case-id")
         case_id = next(iter(cases))
     if case_id not in cases:
-        raise CaseError(f"{op} has no case {case_id!r}; have {sorted(cases)}")
+        raise CaseError(f"{op}: case {case_id!r} is not listed (listed: {', '.join(sorted(cases))})")
     task = cases[case_id]["impls"][0]["task"]
     return load_case_module(Path(root) / task, op, case_id, rel_tol)
 
@@ -247,10 +260,38 @@ def baseline_from_file(baselines: Dict[str, Any], case: Case) -> Optional[float]
     return None
 
 
+def load_traffic(path: os.PathLike) -> Dict[str, Any]:
+    """Measured HBM traffic per operator: a JSON object (or the first ```json block
+    of a Markdown profile) mapping an operator name to ``{"read_bytes",
+    "write_bytes", "shapes": {forward() name: shape}}``."""
+    text = Path(path).read_text()
+    if "```json" in text:
+        text = text.split("```json", 1)[1].split("```", 1)[0]
+    data = json.loads(text)
+    if not isinstance(data, dict):
+        raise CaseError(f"{path}: expected a JSON object of operators")
+    return data
+
+
+def traffic_for(traffic: Optional[Dict[str, Any]], case: Case, inputs: Dict[str, Any]) -> Optional[Dict[str, Any]]:
+    """The profile's figures for this case, only when they were measured at the
+    same input shapes."""
+    if not traffic:
+        return None
+    ent = traffic.get(case.name) or traffic.get(case.op)
+    if not isinstance(ent, dict) or "read_bytes" not in ent or "write_bytes" not in ent:
+        return None
+    shapes = {k: list(np.shape(v)) for k, v in inputs.items() if np.ndim(v)}
+    want = {k: list(v) for k, v in ent.get("shapes", {}).items()}
+    return ent if want == shapes else None
+
+
 def score_case(case: Case, seeds: Sequence[int], device, warmup: int = 20, iters: int = 100,
-               baselines: Optional[Dict[str, Any]] = None, time_it: bool = True) -> Result:
-    """Correctness on every seed, then p50 latency and speedup on the last seed."""
-    from . import harness
+               baselines: Optional[Dict[str, Any]] = None, time_it: bool = True,
+               traffic: Optional[Dict[str, Any]] = None) -> Result:
+    """Correctness on every seed, then p50 latency, roofline metrics and speedup on
+    the last seed."""
+    from . import harness, roofline
     res = Result(op=case.op, case=case.case_id, passed=False, latency_ms=None,
                  seeds=list(seeds), rel_tol=case.rel_tol)
     call = inputs = None
@@ -273,6 +314,11 @@ def score_case(case: Case, seeds: Sequence[int], device, warmup: int = 20, iters
         t = harness.time_op(lambda i: call(), warmup=warmup, iters=iters, device=device)
         res.latency_ms = t.p50_ms
         res.summary_metrics = {"p10_ms": t.p10_ms, "p90_ms": t.p90_ms, "reps": t.samples}
+        # the work model reads the operator's own parameter names; a case module's
+        # forward() may name them differently, so map them by position
+        named = dict(zip(OPS[case.op][1], inputs.values()))
+        res.summary_metrics.update(roofline.metrics(case.op, named, t.p50_ms * 1e-3,
+                                                    traffic_for(traffic, case, inputs)))
         base = baseline_from_file(baselines, case) if baselines else None
         if base is not None:
             res.baseline_latency_ms, res.baseline_kind = base, "baselines.json"
@@ -298,6 +344,31 @@ def line(r: Result) -> str:
             f"(tol {r.rel_tol:g}, seeds {r.seeds}){err}")
 
 
+def digest_line(r: Result) -> str:
+    """The one-line bottleneck digest of an op's summary_metrics (empty if untimed)."""
+    from . import roofline
+    d = roofline.digest(r.summary_metrics)
+    return f"  digest: {d}" if d else ""
+
+
+def build_baselines(cases: Sequence[Case], path: os.PathLike, seed: int = 42,
+                    reps: int = 3) -> Dict[str, Any]:
+    """Measures every case's baseline (its numpy forward on this host, p50 of
+    `reps` after one warm-up, on the inputs of `seed`) and merges the entries into
+    the baselines file in the reference's format (verify.py:23,57-59)."""
+    path = Path(path)
+    data: Dict[str, Any] = json.loads(path.read_text()) if path.exists() else {}
+    cores = len(os.sched_getaffinity(0))
+    for c in cases:
+        inputs = c.draw(seed)
+        ms = time_host(lambda: c.forward(**inputs), reps)
+        data[c.name] = {"baseline_latency_ms": ms, "case_id": c.case_id,
+                        "kernel": f"{c.module_path.name}::forward (host numpy, {cores} cores)",
+                        "op": c.op}
+    path.write_text(json.dumps(data, indent=2, sort_keys=True) + "\n")
+    return data
+
+
 # ----------------------------------------------------------------- CLI
 
 def _parse(argv: Optional[List[str]]) -> argparse.Namespace:
@@ -316,6 +387,10 @@ def _parse(argv: Optional[List[str]]) -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--iters", type=int, default=100)
     ap.add_argument("--baselines", default=None, help="baselines.json (speedup denominators)")
+    ap.add_argument("--build-baselines", action="store_true",
+                    help="measure each case's baseline and write it to --baselines (default baselines.json)")
+    ap.add_argument("--traffic", default=None,
+                    help="measured HBM bytes per op (JSON, or a Markdown profile with a json block)")
     ap.add_argument("--ledger", default=None, help="append results to <DIR>/<op>/benchmark.csv")
     ap.add_argument("--candidate", default=None, help="candidate name recorded in the ledger")
     ap.add_argument("--parent", default="", help="parent name recorded in the ledger")
@@ -349,14 +424,32 @@ def main(argv: Optional[List[str]] = None) -> int:
     seeds = FAST_SEEDS if args.fast else (
         [int(s) for s in args.seeds.split(",")] if args.seeds else SEEDS)
     iters = min(args.iters, 20) if args.fast else args.iters
+    if args.build_baselines:
+        path = args.baselines or "baselines.json"
+        try:
+            data = build_baselines(cases, path)
+        except Exception as e:
+            print(f"verify: baseline measurement failed: {type(e).__name__}: {e}", file=sys.stderr)
+            return 1
+        for c in cases:
+            e = data[c.name]
+            print(f"BASELINE {c.name}  {e['baseline_latency_ms']:.4f} ms  ({e['kernel']})")
+        print(f"{len(cases)} baselines written to {path}")
+        return 0
     baselines = json.loads(Path(args.baselines).read_text()) if args.baselines else None
+    try:
+        traffic = load_traffic(args.traffic) if args.traffic else None
+    except (OSError, ValueError) as e:
+        print(f"verify: cannot read --traffic: {e}", file=sys.stderr)
+        return 2
 
     import torch
     if not torch.cuda.is_available():
         print("verify: no GPU visible", file=sys.stderr)
         return 1
     device = torch.device("cuda", 0)
-    results = [score_case(c, seeds, device, args.warmup, iters, baselines) for c in cases]
+    results = [score_case(c, seeds, device, args.warmup, iters, baselines, traffic=traffic)
+               for c in cases]
 
     if args.ledger:
         from . import _lib, ledger
@@ -367,7 +460,7 @@ def main(argv: Optional[List[str]] = None) -> int:
                 latency_ms=r.latency_ms, speedup=r.speedup, seeds=r.seeds,
                 verdict="scored" if not args.fast else "fast-screen",
                 notes=(r.error or f"rel_l2_max {max(r.rel_l2.values()):.3e}; "
-                       f"baseline {r.baseline_kind}"),
+                       f"baseline {r.baseline_kind}; {digest_line(r).strip()}"),
                 baseline_latency_ms=r.baseline_latency_ms,
                 metrics=r.summary_metrics, case_id=r.case, case_module=str(c.module_path),
                 per_seed_rel_l2={str(k): v for k, v in r.rel_l2.items()}))
@@ -377,6 +470,8 @@ def main(argv: Optional[List[str]] = None) -> int:
     else:
         for r in results:
             print(line(r))
+            if digest_line(r):
+                print(digest_line(r))
         g = geomean([r.speedup for r in results if r.passed and r.speedup])
         npass = sum(r.passed for r in results)
         print(f"{npass}/{len(results)} passed; geomean speedup "

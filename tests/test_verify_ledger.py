@@ -38,9 +38,9 @@ def test_seeds_draw_distinct_but_reproducible_inputs():
 def test_resolve_case_through_summary_json():
     c = verify.resolve_case(CASES, "matmul")
     assert c.case_id == "1" and c.module_path.name == "matmul_small.py"
-    with pytest.raises(verify.CaseError, match="not in summary.json"):
+    with pytest.raises(verify.CaseError, match="lists no operator 'bmm'"):
         verify.resolve_case(CASES, "bmm")
-    with pytest.raises(verify.CaseError, match="no case"):
+    with pytest.raises(verify.CaseError, match="case '7' is not listed"):
         verify.resolve_case(CASES, "matmul", "7")
 
 
@@ -94,6 +94,82 @@ def test_baseline_lookup_in_reference_format():
     assert verify.baseline_from_file({"matmul": {"baseline_latency_ms": 2.0}}, c) is None
 
 
+def test_build_baselines_writes_reference_format(tmp_path, capsys):
+    """--build-baselines runs on the host alone (no GPU): each case's numpy forward,
+    timed, written as {"op[case=id]": {baseline_latency_ms, case_id, kernel, op}}
+    (the reference's baselines.json format), merged into an existing file, and read
+    back as the speedup denominator."""
+    path = tmp_path / "baselines.json"
+    path.write_text(json.dumps({"other[case=0]": {"baseline_latency_ms": 9.0, "case_id": "0",
+                                                  "kernel": "k.py", "op": "other"}}))
+    rc = verify.main(["--nkibench-root", str(CASES), "--build-baselines", "--baselines", str(path)])
+    out = capsys.readouterr().out
+    assert rc == 0 and out.count("BASELINE ") == 3 and "3 baselines written" in out
+    data = json.loads(path.read_text())
+    assert set(data) == {"other[case=0]", "silu[case=1]", "matmul[case=1]", "add_rmsnorm_matmul[case=1]"}
+    ent = data["matmul[case=1]"]
+    assert set(ent) == {"baseline_latency_ms", "case_id", "kernel", "op"}
+    assert ent["case_id"] == "1" and ent["op"] == "matmul" and ent["baseline_latency_ms"] > 0
+    assert ent["kernel"].startswith("matmul_small.py::forward (host numpy")
+    c = verify.resolve_case(CASES, "matmul")
+    assert verify.baseline_from_file(data, c) == ent["baseline_latency_ms"]
+
+
+class _Shape:
+    def __init__(self, *shape):
+        self.shape = shape
+
+
+def test_roofline_work_matches_the_bench_tables():
+    """kda.roofline's work per call, from forward() shapes, equals bench.py's
+    NKIBench table (work, bound, fp32-equivalent flops) at every NKIBench shape."""
+    import bench
+    from kda import roofline
+    for op, cfg in bench.NKIBENCH.items():
+        names = verify.OPS[op][1]
+        shapes = bench._nki_shapes(op, cfg["dims"])
+        arrays = [n for n in names if n != "eps"]
+        assert len(arrays) == len(shapes), op
+        inputs = {n: _Shape(*sh) for n, sh in zip(arrays, shapes)}
+        w = roofline.op_work(op, inputs)
+        assert w.bound == cfg["bound"] and w.work == cfg["work"], op
+        if "useful" in cfg:
+            assert w.useful_flops == cfg["useful"], op
+
+
+def test_roofline_metrics_and_digest():
+    from kda import roofline
+    m = roofline.metrics("silu", {"x": _Shape(2048, 8192)}, 24e-6)
+    assert m["bound"] == "hbm" and m["unit"] == "GB/s"
+    assert math.isclose(m["achieved"], 2048 * 8192 * 8 / 24e-6 / 1e9)
+    assert math.isclose(m["roofline_frac"], 2048 * 8192 * 8 / 24e-6 / 8e12)
+    assert roofline.digest(m) == "HBM 5.59 TB/s = 0.70 of 8 TB/s; HBM algorithmic 134.2MB"
+    m = roofline.metrics("matmul", {"lhs": _Shape(4096, 5120), "rhs": _Shape(5120, 12288)}, 1.25e-3,
+                         {"read_bytes": 512.0e6, "write_bytes": 201.3e6})
+    f = 2 * 4096 * 5120 * 12288
+    assert math.isclose(m["roofline_frac"], 3 * f / 1.25e-3 / 2.5e15)
+    assert math.isclose(m["fp32_tflops"], f / 1.25e-3 / 1e12)
+    d = roofline.digest(m)
+    assert d.startswith("MFMA 1237 TFLOP/s issued = 0.49 of 2.5 PFLOP/s; fp32-equivalent 412 TFLOP/s")
+    assert "HBMrd=512.0MB HBMwr=201.3MB" in d
+    tiny = roofline.metrics("matmul", {"lhs": _Shape(128, 256), "rhs": _Shape(256, 192)}, 22.5e-6)
+    assert roofline.digest(tiny).startswith("MFMA 1.68 TFLOP/s issued = 0.000671 of 2.5 PFLOP/s")
+    with pytest.raises(KeyError):
+        roofline.op_work("conv", {})
+
+
+def test_traffic_applies_only_at_its_shapes(tmp_path):
+    c = verify.load_case_module(CASES / "silu_small.py", "silu")
+    prof = tmp_path / "traffic.md"
+    prof.write_text("# profile\n\n```json\n" + json.dumps(
+        {"silu": {"read_bytes": 256000, "write_bytes": 256000, "shapes": {"x": [64, 1000]}}}) + "\n```\n")
+    t = verify.load_traffic(prof)
+    inputs = c.draw(0)
+    assert verify.traffic_for(t, c, inputs)["read_bytes"] == 256000
+    assert verify.traffic_for(t, c, {"x": np.zeros((64, 999), np.float32)}) is None
+    assert verify.traffic_for(None, c, inputs) is None
+
+
 def test_ledger_rows_and_summary(tmp_path):
     full = verify.SEEDS
     recs = [
@@ -128,8 +204,13 @@ def test_verify_cli_end_to_end(tmp_path, capsys):
     print(out)
     assert rc == 0
     assert out.count("PASS ") == 3 and "geomean speedup" in out
+    assert out.count("  digest: ") == 3
+    assert "  digest: MFMA " in out and "  digest: HBM " in out
     s = ledger.summarize(tmp_path)
     assert s["n_with_validated"] == 3
+    rec = json.loads((tmp_path / "matmul" / "candidates.jsonl").read_text().splitlines()[0])
+    assert rec["metrics"]["bound"] == "mfma" and 0 < rec["metrics"]["roofline_frac"] < 1
+    assert "digest: MFMA" in rec["notes"]
 
 
 @pytest.mark.gpu
