@@ -44,6 +44,7 @@
 //   The second wave of each SIMD
 //   runs at a raised issue priority so both reach the per-iteration barrier
 //   together.
+#include "attention_geom.h"
 #include "common.h"
 #include "lanes.h"
 #include "lds_dma.h"
@@ -51,37 +52,12 @@
 namespace kda {
 namespace attn {
 
-constexpr int kD = 128;       // head dim
-constexpr int kWaveRows = 32; // query rows per wave
+// Sizes, launch arguments and every global address (q loads, K/V tile DMAs,
+// output stores) come from attention_geom.h.
 constexpr int kIT = kWaveRows / 16;
-constexpr int kBN = 64;       // keys per tile
-constexpr int kWaves = 8;     // per workgroup: HPW query heads x (8 / HPW) blocks of 32 rows
-constexpr int kThreads = 64 * kWaves;
-constexpr int kTileBytes = kBN * kD * 2;                    // one K or V tile: 16 KiB
-// The K/V DMAs are issued by waves 0-3 only: they are served first by the
-// instruction arbiter of their SIMDs and otherwise wait at the barrier for the
-// second wave of each SIMD, so the issue work moves off the slower waves.
-constexpr int kDmaWaves = kWaves / 2;
-constexpr int kDmaPerWave = kTileBytes / (kDmaWaves * 1024);   // DMA instructions per issuing wave per tile
 constexpr int kDT = kD / 16;                                // O^T tiles along d
 constexpr float kLazy = 8.0f;  // running-max slack (log2 units) before O is rescaled
 constexpr int kRing = 4;       // K and V tile slots in LDS (a power of two: slot = kt & 3)
-
-struct Args {
-  const uint16_t* q;   // [B][S][Hq][D] (strides below, in elements)
-  const uint16_t* k;   // [B][S][Hkv][D]
-  const uint16_t* v;
-  uint16_t* out;
-  int64_t q_sb, q_ss;  // batch / sequence strides of q (head stride is D)
-  int64_t k_sb, k_ss;
-  int64_t o_sb, o_ss, o_sh;
-  int batch, seq, hq, hkv;
-  float scale_log2;    // softmax scale * log2(e)
-};
-
-// Swizzle of the 16 16-byte chunks of a K row: conflict-free for the permuted
-// 16-row fragment read (rows 32c + 8a + 4hh + r, a, r in 0..3, one chunk).
-__device__ __forceinline__ int kswz(int row) { return (row & 3) | (((row >> 3) & 3) << 2); }
 
 typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -312,7 +288,6 @@ __device__ __forceinline__ void probs_then_scores(State& st, const uint8_t* k_ld
 // kv head's G query heads are spread over G / HPW workgroups.
 template <bool CAUSAL, int HPW>
 __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
-  constexpr int kBM = kWaveRows * kWaves / HPW;
   __shared__ __align__(1024) uint8_t smem[2 * kRing * kTileBytes];   // K slots, then V slots
 
   const int tid = threadIdx.x;
@@ -321,18 +296,10 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   const int l16 = lane & 15;
   const int g = lane >> 4;
 
-  const int nqb = (p.seq + kBM - 1) / kBM;
-  const int group = p.hq / p.hkv;
-  const int nsplit = group / HPW;                   // workgroups per kv head
-  const int nbh = p.batch * p.hkv * nsplit;
-  // Longest causal blocks first.
-  const int qb = CAUSAL ? (nqb - 1 - (int)blockIdx.x / nbh) : ((int)blockIdx.x / nbh);
-  const int bh = blockIdx.x % nbh;
-  const int b = bh / (p.hkv * nsplit);
-  const int kvh = (bh / nsplit) % p.hkv;
-  const int h = kvh * group + (bh % nsplit) * HPW + (wave % HPW);
-  const int q0 = qb * kBM;
-  const int w0 = q0 + (wave / HPW) * kWaveRows;     // this wave's first query row
+  // (batch, kv head, query head, rows) of this workgroup and wave; causal
+  // blocks with the most key tiles first
+  const Block blk = block_of(p, CAUSAL, HPW, (int)blockIdx.x, wave);
+  const int w0 = blk.w0;                            // this wave's first query row
 
   // The instruction arbiter serves the older waves (0-3) of each SIMD first, and
   // they also issue the K/V DMAs; the younger waves get a higher issue priority
@@ -341,14 +308,14 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   State st;
   {
     // Q fragments, scaled by scale*log2(e) and rounded to bf16 once
-    const uint16_t* qp = p.q + b * p.q_sb + (int64_t)h * kD;
+    const uint16_t* qp = p.q + q_head(p, blk);
 #pragma unroll
     for (int it = 0; it < kIT; ++it) {
       const int row = w0 + it * 16 + l16;
 #pragma unroll
       for (int dc = 0; dc < 4; ++dc) {
         const u32x4 raw = (row < p.seq)
-                              ? *reinterpret_cast<const u32x4*>(qp + row * p.q_ss + dc * 32 + g * 8)
+                              ? *reinterpret_cast<const u32x4*>(qp + q_elem(p, row, dc, g))
                               : u32x4{0u, 0u, 0u, 0u};
         u32x4 w;
 #pragma unroll
@@ -370,23 +337,17 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   // ---- DMA geometry: instruction j of issuing wave w (< kDmaWaves) fills LDS
   // bytes [(j*kDmaWaves + w)*1024, +1024) of a tile = rows 4q .. 4q+3, lane -> (row, chunk)
   const int64_t row_bytes = p.k_ss * 2;
-  const char* kbase = uniform_ptr(p.k + b * p.k_sb + (int64_t)kvh * kD);
-  const char* vbase = uniform_ptr(p.v + b * p.k_sb + (int64_t)kvh * kD);
+  const char* kbase = uniform_ptr(p.k + kv_head(p, blk));
+  const char* vbase = uniform_ptr(p.v + kv_head(p, blk));
   // Per-lane byte offsets within a tile (row * row_bytes + swizzled chunk) are
   // loop invariants; the LDS destination of each instruction is wave-uniform.
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  auto dma_row = [&](int j) { return (j * kDmaWaves + wave % kDmaWaves) * 4 + (lane >> 4); };
-  auto kcol = [&](int r) { return (uint32_t)(((lane & 15) ^ kswz(r)) << 4); };
-  auto vcol = [&](int r) {
-    const int t = lane & 15;
-    return (uint32_t)((((t >> 1) ^ mswz(r)) << 5) + ((t & 1) << 4));
-  };
   uint32_t koff[kDmaPerWave], voff[kDmaPerWave];
 #pragma unroll
   for (int j = 0; j < kDmaPerWave; ++j) {
-    const int r = dma_row(j);
-    koff[j] = (uint32_t)(r * row_bytes) + kcol(r);
-    voff[j] = (uint32_t)(r * row_bytes) + vcol(r);
+    const int r = dma_row(j, wave, lane);
+    koff[j] = dma_lane_offset(row_bytes, r, dma_kcol(r, lane));
+    voff[j] = dma_lane_offset(row_bytes, r, dma_vcol(r, lane));
   }
   // Rows past the sequence (only in the last, partial tile) are clamped to the
   // last key: their scores are masked and their V rows meet p = 0.
@@ -400,11 +361,10 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
       for (int j = 0; j < kDmaPerWave; ++j)
         dma16(tb, off[j], lds + (uint32_t)((j * kDmaWaves + wave_u) * 1024));
     } else {
-      const int last = p.seq - 1 - j0;
 #pragma unroll
       for (int j = 0; j < kDmaPerWave; ++j) {
-        const int r = dma_row(j);
-        dma16(tb, (uint32_t)(min(r, last) * row_bytes) + (is_v ? vcol(r) : kcol(r)),
+        const int r = dma_row(j, wave, lane);
+        dma16(tb, dma_lane_offset(row_bytes, dma_src_row(p, kt, r), is_v ? dma_vcol(r, lane) : dma_kcol(r, lane)),
               lds + (uint32_t)((j * kDmaWaves + wave_u) * 1024));
       }
     }
@@ -412,12 +372,8 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   auto k_tile = [&](int kt) { return smem + (kt % kRing) * kTileBytes; };
   auto v_tile = [&](int kt) { return smem + (kRing + kt % kRing) * kTileBytes; };
 
-  const int nkt_all = (p.seq + kBN - 1) / kBN;
-  const int nkt = CAUSAL ? min(nkt_all, (q0 + kBM - 1) / kBN + 1) : nkt_all;
-  // tiles [0, nfree) need no mask for any row of this workgroup
-  int nfree = p.seq / kBN;                         // full tiles
-  if (CAUSAL) nfree = min(nfree, (q0 + 1) / kBN);  // keys j0+63 <= q0 for every row
-  nfree = min(nfree, nkt);
+  const int nkt = blk.nkt;
+  const int nfree = blk.nfree;   // tiles [0, nfree) need no mask for any row of this workgroup
 
   // Iteration kt (after the barrier that ends iteration kt-1) fetches K(kt+3) into
   // the slot of K(kt-1) and V(kt+1) into the slot of V(kt-3) (both last read in
@@ -425,9 +381,8 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   // S(kt).  Each DMA has two iterations to land: the barrier that ends iteration
   // kt waits only for the DMAs issued in iteration kt-1 (K(kt+2), V(kt)), which
   // iteration kt+1 reads.
-  issue(kbase, false, koff, 0, lds_addr(k_tile(0)));
-  issue(kbase, false, koff, min(1, nkt - 1), lds_addr(k_tile(1)));
-  issue(kbase, false, koff, min(2, nkt - 1), lds_addr(k_tile(2)));
+#pragma unroll
+  for (int i = 0; i < kPrologueK; ++i) issue(kbase, false, koff, prologue_k_tile(i, nkt), lds_addr(k_tile(i)));
   issue(vbase, true, voff, 0, lds_addr(v_tile(0)));
   wait_vmcnt<0>();
   __syncthreads();
@@ -442,8 +397,8 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   // no longer read, so every iteration issues the same number of DMAs and the
   // wait below has a fixed count.
   auto fetch = [&](int kt) {
-    issue(kbase, false, koff, min(kt + 3, nkt - 1), lds_addr(k_tile(kt + 3)));
-    issue(vbase, true, voff, min(kt + 1, nkt - 1), lds_addr(v_tile(kt + 1)));
+    issue(kbase, false, koff, k_fetch_tile(kt, nkt), lds_addr(k_tile(kt + 3)));
+    issue(vbase, true, voff, v_fetch_tile(kt, nkt), lds_addr(v_tile(kt + 1)));
   };
   // O moves to the running max set by the previous tile's statistics; done
   // before the next O += V P (and at the top of an iteration, so the branch does
@@ -516,7 +471,7 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
 
   // ---- normalise and store: lane holds out[row][d = dt*16 + 4g .. +4]; the
   // row sum is the sum of the four lanes' parts
-  uint16_t* op = p.out + b * p.o_sb + (int64_t)h * p.o_sh;
+  uint16_t* op = p.out + out_head(p, blk);
 #pragma unroll
   for (int it = 0; it < kIT; ++it) {
     const float inv = 1.0f / row_sum4(st.l[it]);
@@ -528,7 +483,7 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
       u32x2 w;
       w[0] = pack2(o[0], o[1]);
       w[1] = pack2(o[2], o[3]);
-      *reinterpret_cast<u32x2*>(op + row * p.o_ss + dt * 16 + 4 * g) = w;
+      *reinterpret_cast<u32x2*>(op + out_elem(p, row, dt, g)) = w;
     }
   }
 }
@@ -562,37 +517,21 @@ extern "C" int kda_gqa_fwd_bf16(const kda_bf16* q, const kda_bf16* k, const kda_
     return set_error(KDA_ERR_INVALID_ARG, "gqa_fwd_bf16: q/k/v must be 16-byte, out 8-byte aligned");
   if ((out_stride_s % 4) || (out_stride_h % 4) || (out_stride_b % 4))
     return set_error(KDA_ERR_INVALID_ARG, "gqa_fwd_bf16: output strides must be multiples of 4");
-  // heads per workgroup: the largest power of two up to 8 that divides the group
-  const int64_t group = hq / hkv;
-  const int hpw = (group % 8 == 0) ? 8 : (group % 4 == 0) ? 4 : (group % 2 == 0) ? 2 : 1;
-  const int64_t bm = kWaveRows * kWaves / hpw;
-  const int64_t nblocks = ((seq + bm - 1) / bm) * batch * hkv * (group / hpw);
+  const int hpw = heads_per_workgroup(hq / hkv);
+  const int64_t nblocks = grid_blocks(batch, seq, hq, hkv);
   if (nblocks > 0x7fffffff || seq > (1 << 30) || hq > (1 << 20))
     return set_error(KDA_ERR_UNSUPPORTED, "gqa_fwd_bf16: problem too large");
   // The K/V DMAs address a tile's rows from a scalar base with 32-bit per-lane
-  // byte offsets (row * Hkv*D*2 + chunk, rows 0..63 of a tile).
-  if ((kBN - 1) * (hkv * kD * 2) + 2 * kD > (int64_t)0xffffffff)
+  // byte offsets (row * Hkv*D*2 + chunk start; rows 0..63, chunks start at most
+  // 2*D - 16 bytes into a row).
+  if ((kBN - 1) * (hkv * kD * 2) + (2 * kD - 16) > (int64_t)0xffffffff)
     return set_error(KDA_ERR_UNSUPPORTED,
                      "gqa_fwd_bf16: Hkv=%lld kv heads exceed the 32-bit DMA offsets of a key tile",
                      (long long)hkv);
 
-  Args a;
-  a.q = q;
-  a.k = k;
-  a.v = v;
-  a.out = out;
-  a.q_ss = hq * kD;
-  a.q_sb = seq * a.q_ss;
-  a.k_ss = hkv * kD;
-  a.k_sb = seq * a.k_ss;
-  a.o_sb = out_stride_b;
-  a.o_ss = out_stride_s;
-  a.o_sh = out_stride_h;
-  a.batch = (int)batch;
-  a.seq = (int)seq;
-  a.hq = (int)hq;
-  a.hkv = (int)hkv;
-  a.scale_log2 = scale * 1.4426950408889634f;
+  const Args a = make_args(reinterpret_cast<const uint16_t*>(q), reinterpret_cast<const uint16_t*>(k),
+                           reinterpret_cast<const uint16_t*>(v), reinterpret_cast<uint16_t*>(out), batch,
+                           seq, hq, hkv, scale, out_stride_b, out_stride_s, out_stride_h);
   hipStream_t st = as_stream(stream);
   const dim3 grid((unsigned)nblocks), block(kThreads);
 #define KDA_GQA_LAUNCH(H)                                                         \

@@ -1,0 +1,173 @@
+// Address geometry of the bf16 GQA forward kernel (attention.hip): which
+// (batch, kv head, query head, rows) a workgroup and wave own, how many key tiles
+// a workgroup visits, and the global byte offsets of its q loads, K/V tile DMAs
+// and output stores.  The functions are host and device code: the kernel computes
+// every global address through them, and a host-side replay (tests/) walks the
+// same functions over every workgroup, wave and lane of a launch to check that
+// each access stays inside its buffer.
+#pragma once
+
+#include <stdint.h>
+
+#include "common.h"
+#include "lds_dma.h"
+
+namespace kda {
+namespace attn {
+
+constexpr int kD = 128;       // head dim
+constexpr int kWaveRows = 32; // query rows per wave
+constexpr int kBN = 64;       // keys per tile
+constexpr int kWaves = 8;     // per workgroup: HPW query heads x (8 / HPW) blocks of 32 rows
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTileBytes = kBN * kD * 2;                    // one K or V tile: 16 KiB
+// The K/V DMAs are issued by waves 0-3 only: they are served first by the
+// instruction arbiter of their SIMDs and otherwise wait at the barrier for the
+// second wave of each SIMD, so the issue work moves off the slower waves.
+constexpr int kDmaWaves = kWaves / 2;
+constexpr int kDmaPerWave = kTileBytes / (kDmaWaves * 1024);   // DMA instructions per issuing wave per tile
+
+struct Args {
+  const uint16_t* q;   // [B][S][Hq][D] (strides below, in elements)
+  const uint16_t* k;   // [B][S][Hkv][D]
+  const uint16_t* v;
+  uint16_t* out;
+  int64_t q_sb, q_ss;  // batch / sequence strides of q (head stride is D)
+  int64_t k_sb, k_ss;
+  int64_t o_sb, o_ss, o_sh;
+  int batch, seq, hq, hkv;
+  float scale_log2;    // softmax scale * log2(e)
+};
+
+// The launch's arguments for dense BSHD q/k/v and output strides (elements).
+inline Args make_args(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
+                      int64_t batch, int64_t seq, int64_t hq, int64_t hkv, float scale,
+                      int64_t o_sb, int64_t o_ss, int64_t o_sh) {
+  Args a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.q_ss = hq * kD;
+  a.q_sb = seq * a.q_ss;
+  a.k_ss = hkv * kD;
+  a.k_sb = seq * a.k_ss;
+  a.o_sb = o_sb;
+  a.o_ss = o_ss;
+  a.o_sh = o_sh;
+  a.batch = (int)batch;
+  a.seq = (int)seq;
+  a.hq = (int)hq;
+  a.hkv = (int)hkv;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  return a;
+}
+
+// Heads per workgroup: the largest power of two up to 8 dividing G = Hq / Hkv.
+__host__ __device__ __forceinline__ int heads_per_workgroup(int64_t group) {
+  return (group % 8 == 0) ? 8 : (group % 4 == 0) ? 4 : (group % 2 == 0) ? 2 : 1;
+}
+__host__ __device__ __forceinline__ constexpr int block_rows(int hpw) { return kWaveRows * kWaves / hpw; }
+
+__host__ __device__ __forceinline__ int imin(int a, int b) { return a < b ? a : b; }
+
+// Workgroups of a launch: query blocks x batch x kv heads x workgroups per kv head.
+inline int64_t grid_blocks(int64_t batch, int64_t seq, int64_t hq, int64_t hkv) {
+  const int hpw = heads_per_workgroup(hq / hkv);
+  const int64_t bm = block_rows(hpw);
+  return ((seq + bm - 1) / bm) * batch * hkv * (hq / hkv / hpw);
+}
+
+// What workgroup `block`, wave `wave` owns.
+struct Block {
+  int b, kvh, h;   // batch, kv head, this wave's query head
+  int q0, w0;      // the workgroup's first query row, this wave's first query row
+  int nkt;         // key tiles the workgroup visits (0 .. nkt-1)
+  int nfree;       // tiles [0, nfree) need no mask for any row of the workgroup
+};
+
+__host__ __device__ __forceinline__ Block block_of(const Args& p, bool causal, int hpw, int block, int wave) {
+  const int bm = block_rows(hpw);
+  const int nqb = (p.seq + bm - 1) / bm;
+  const int group = p.hq / p.hkv;
+  const int nsplit = group / hpw;                   // workgroups per kv head
+  const int nbh = p.batch * p.hkv * nsplit;
+  Block r;
+  // Longest causal blocks first.
+  const int qb = causal ? (nqb - 1 - block / nbh) : (block / nbh);
+  const int bh = block % nbh;
+  r.b = bh / (p.hkv * nsplit);
+  r.kvh = (bh / nsplit) % p.hkv;
+  r.h = r.kvh * group + (bh % nsplit) * hpw + (wave % hpw);
+  r.q0 = qb * bm;
+  r.w0 = r.q0 + (wave / hpw) * kWaveRows;
+  const int nkt_all = (p.seq + kBN - 1) / kBN;
+  r.nkt = causal ? imin(nkt_all, (r.q0 + bm - 1) / kBN + 1) : nkt_all;
+  int nfree = p.seq / kBN;                            // full tiles
+  if (causal) nfree = imin(nfree, (r.q0 + 1) / kBN);  // keys j0+63 <= q0 for every row
+  r.nfree = imin(nfree, r.nkt);
+  return r;
+}
+
+// Element offsets of a workgroup's q head, K/V kv head and output head.
+__host__ __device__ __forceinline__ int64_t q_head(const Args& p, const Block& g) {
+  return g.b * p.q_sb + (int64_t)g.h * kD;
+}
+__host__ __device__ __forceinline__ int64_t kv_head(const Args& p, const Block& g) {
+  return g.b * p.k_sb + (int64_t)g.kvh * kD;
+}
+__host__ __device__ __forceinline__ int64_t out_head(const Args& p, const Block& g) {
+  return g.b * p.o_sb + (int64_t)g.h * p.o_sh;
+}
+// Element offset, from q_head, of the 8 q values lane (l16, g) loads for query
+// `row` and d chunk dc (d = dc*32 + 8g .. +8); loaded only when row < seq.
+__host__ __device__ __forceinline__ int64_t q_elem(const Args& p, int row, int dc, int g) {
+  return row * p.q_ss + dc * 32 + g * 8;
+}
+// Element offset, from out_head, of the 4 outputs lane (l16, g) stores for query
+// `row` and d tile dt (d = dt*16 + 4g .. +4); stored only when row < seq.
+__host__ __device__ __forceinline__ int64_t out_elem(const Args& p, int row, int dt, int g) {
+  return row * p.o_ss + dt * 16 + 4 * g;
+}
+
+// ---- K/V tile DMAs: instruction j of issuing wave w (< kDmaWaves) fills LDS
+// bytes [(j*kDmaWaves + w)*1024, +1024) of a tile = rows 4q .. 4q+3, 16 bytes per
+// lane: lane -> (row, 16-byte chunk position lane & 15).
+__host__ __device__ __forceinline__ int dma_row(int j, int wave, int lane) {
+  return (j * kDmaWaves + wave % kDmaWaves) * 4 + (lane >> 4);
+}
+// Swizzle of the 16 16-byte chunks of a K row: conflict-free for the permuted
+// 16-row fragment read (rows 32c + 8a + 4hh + r, a, r in 0..3, one chunk).
+__host__ __device__ __forceinline__ int kswz(int row) { return (row & 3) | (((row >> 3) & 3) << 2); }
+// Byte offset within a source row of the chunk that lane's DMA places at its
+// position (the LDS swizzle applied on the global side).
+__host__ __device__ __forceinline__ uint32_t dma_kcol(int r, int lane) {
+  return (uint32_t)(((lane & 15) ^ kswz(r)) << 4);
+}
+__host__ __device__ __forceinline__ uint32_t dma_vcol(int r, int lane) {
+  const int t = lane & 15;
+  return (uint32_t)((((t >> 1) ^ mswz(r)) << 5) + ((t & 1) << 4));   // V keeps mswz segments
+}
+// Per-lane 32-bit byte offset, from the tile's first key row, of source row `r`
+// (the launcher bounds Hkv so that rows 0..63 never wrap it).
+__host__ __device__ __forceinline__ uint32_t dma_lane_offset(int64_t row_bytes, int r, uint32_t col) {
+  return (uint32_t)(r * row_bytes) + col;
+}
+// The key tiles a workgroup's DMAs fetch: before the loop K(0), K(1), K(2) and
+// V(0); iteration kt (0 .. nkt-1) fetches K(kt+3) and V(kt+1).  Past the last
+// tile the last tile is fetched again (into a slot no longer read), so every
+// iteration issues the same number of DMAs.
+constexpr int kPrologueK = 3;
+__host__ __device__ __forceinline__ int k_fetch_tile(int kt, int nkt) { return imin(kt + 3, nkt - 1); }
+__host__ __device__ __forceinline__ int v_fetch_tile(int kt, int nkt) { return imin(kt + 1, nkt - 1); }
+__host__ __device__ __forceinline__ int prologue_k_tile(int i, int nkt) { return imin(i, nkt - 1); }
+
+// Source row of tile row r in key tile kt: rows past the sequence (only in the
+// last, partial tile) are clamped to the last key.
+__host__ __device__ __forceinline__ int dma_src_row(const Args& p, int kt, int r) {
+  const int j0 = kt * kBN;
+  return (j0 + kBN <= p.seq) ? r : imin(r, p.seq - 1 - j0);
+}
+
+}  // namespace attn
+}  // namespace kda

@@ -52,7 +52,7 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 
 // Position of 32-byte segment s of k-row k in an MN-contiguous tile of at least
 // 8 segments per row (measured conflict-free for the fragment read below).
-__device__ __forceinline__ int mswz(int k) { return (k & 3) | (((k >> 3) & 1) << 2); }
+__host__ __device__ __forceinline__ int mswz(int k) { return (k & 3) | (((k >> 3) & 1) << 2); }
 
 // Reads the MFMA fragment (column `col0 + lane%16`, k = kbase + 8*(lane/16) .. +7)
 // of an MN-contiguous [k][COLS] bf16 tile (segment s of row k at s ^ mswz(k));

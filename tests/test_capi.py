@@ -109,10 +109,11 @@ def test_missing_workspace_refused_at_large_shapes():
 
 def test_gqa_bf16_rejects_kv_heads_beyond_32bit_dma_offsets():
     """A key tile's 64 rows are addressed with 32-bit per-lane byte offsets
-    (row * Hkv*256 + chunk): Hkv = 266305 would wrap them, 266304 is the largest
-    that fits.  Refused before any launch (the pointers are never dereferenced)."""
+    (row * Hkv*256 + chunk start, at most 63 * Hkv*256 + 240): Hkv = 266306 would
+    wrap them, 266305 is the largest that fits (tests/test_gqa_addresses.py replays
+    both).  Refused before any launch (the pointers are never dereferenced)."""
     fake = 1 << 20
-    for hkv in (266305, 1 << 20):
+    for hkv in (266306, 1 << 20):
         with pytest.raises(ValueError, match="32-bit DMA offsets"):
             _lib.call("kda_gqa_fwd_bf16", fake, fake, fake, fake, 1, 64, hkv, hkv, 128, 0.088, 1,
                       0, 0, 0, None)
