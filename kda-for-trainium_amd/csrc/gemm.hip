@@ -101,6 +101,8 @@ struct Params {
   int64_t batch_a, batch_b, batch_c;   // per-batch strides (elements), batch = blockIdx.y
   int m, n, k;             // k = sum of segment extents
   int group_m;             // tile rows per group of the tile order (set at launch)
+  int* zero;               // zero_n ints that workgroup (0, 0) clears before its tile: the
+  int zero_n;              // flags of a launch that follows on the same stream
 };
 
 // Position of 16-byte chunk c of row r in a K-contiguous tile of BK-element
@@ -139,15 +141,61 @@ __device__ __forceinline__ bf16x8 read_k_frag(const uint8_t* tile, int row, int 
   return *reinterpret_cast<const bf16x8*>(tile + row * (BK * 2) + ((c ^ kswz<BK>(row)) << 4));
 }
 
-template <int BM, int BN, int NB, bool A_KMAJ, Epi EPI, bool KTAIL, int BK, int STAGES, int NSEG>
-__global__ __launch_bounds__(kThreads, 1) void gemm_kernel(Params p) {
+// Wave-tile geometry of a BM x BN (x NB B operands) workgroup tile.
+template <int BM, int BN>
+struct WaveTile {
+  static constexpr int WM = BM / kWavesM, WN = BN / kWavesN;   // wave tile (per B operand)
+  static constexpr int TM = WM / 16, TN = WN / 16;             // 16x16 MFMA tiles per wave
+};
+
+// A dependency of a k-range on other workgroups: before the DMA of k-tile `kt`
+// (and every later one) is issued, *flag must reach `target` (a counter that
+// producer workgroups raise with release semantics after their stores).  The wait
+// is bounded (see wait_flag).  kt < 0: no dependency.
+struct KDep {
+  int kt = -1;
+  const int* flag = nullptr;
+  int target = 0;
+};
+
+// Spins (lane 0, relaxed agent-scope loads) until *flag >= target, then acquires
+// at agent scope so the producers' stores are visible to the loads that follow.
+// Producers are workgroups dispatched before the waiter, so the wait ends; the
+// spin is still bounded (2^21 polls of a memory round trip each, about a second)
+// so that a broken schedule can never hang the device.
+__device__ __forceinline__ void wait_flag(const int* flag, int target) {
+  if ((threadIdx.x & 63) == 0) {
+    for (int i = 0; i < (1 << 21); ++i) {
+      if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+// Raises *flag by one once every store of the workgroup so far is visible at
+// agent scope: each wave waits for its own stores to reach the L2, and after the
+// barrier one release increment (which writes the L2 back) publishes them all.
+__device__ __forceinline__ void publish(int* flag) {
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(flag, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The K loop of one output tile (m0, n0) of batch bz: DMA ring, ping-pong MFMA
+// schedule, fp32 accumulators left in acc.  With DEP, wave 0 waits on dep.flag
+// before the barrier that precedes the first issue of k-tile dep.kt.
+template <int BM, int BN, int NB, bool A_KMAJ, bool KTAIL, int BK, int STAGES, int NSEG, bool DEP = false>
+__device__ __forceinline__ void gemm_mainloop(const Params& p, int m0, int n0, int64_t bz, uint8_t* smem,
+                                              floatx4 (&acc)[NB][WaveTile<BM, BN>::TM][WaveTile<BM, BN>::TN],
+                                              KDep dep = {}) {
   static_assert(NSEG >= 1 && NSEG <= kMaxSeg, "segments");
   static_assert(NB == 1 || NB == 2, "one or two B operands");
   static_assert(BM % 128 == 0 && BN % 128 == 0, "tile");
   static_assert(STAGES >= 2, "ring depth");
   static_assert(kWaves == 8, "ping-pong needs 8 waves");
-  constexpr int WM = BM / kWavesM, WN = BN / kWavesN;   // wave tile (per B operand)
-  constexpr int TM = WM / 16, TN = WN / 16;   // 16x16 MFMA tiles per wave
+  constexpr int WM = WaveTile<BM, BN>::WM, WN = WaveTile<BM, BN>::WN;
+  constexpr int TM = WaveTile<BM, BN>::TM, TN = WaveTile<BM, BN>::TN;
   constexpr int NBF = NB * TN;                // B fragments per k-tile per wave
   constexpr int A_BYTES = BM * BK * 2;
   constexpr int B_BYTES = BN * BK * 2;        // per B operand
@@ -161,19 +209,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(Params p) {
   constexpr int A_LPR = 64 / A_RPI;           // lanes per tile row
   constexpr int B_LPR = 64 / B_RPI;
 
-  extern __shared__ __align__(1024) uint8_t smem[];
-
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / kWavesN, wn = wave % kWavesN;
-
-  const int tiles_m = (p.m + BM - 1) / BM, tiles_n = (p.n + BN - 1) / BN;
-  int tm, tn;
-  tile_coords(tiles_m, tiles_n, p.group_m, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
   const int M = p.m, N = p.n, K = p.k;
   const int nk = (K + BK - 1) / BK;
-  const int64_t bz = blockIdx.y;
 
   // ---- DMA sources.  Each lane keeps the (row, column) it fetches; its byte
   // offset from the segment's per-batch base is formed per issue from the
@@ -293,7 +333,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(Params p) {
     }
   };
 
-  floatx4 acc[NB][TM][TN];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
@@ -336,6 +375,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(Params p) {
   constexpr int LEAD = STAGES >= 3 ? 2 : 1;
   constexpr int KH = BK / 32;                   // 32-wide k halves per tile
   const int grp = wave >> 2;
+  // Dependencies need the 2-tile DMA lead: k-tile kt is then issued by group 0 in
+  // the load phase of iteration kt - 2 and by group 1 one phase later.  The
+  // prologue issues tiles 0 and 1 and iteration 0 tile 2, so a dependency on one
+  // of those is awaited (by every wave) before the prologue.
+  static_assert(!DEP || LEAD == 2, "dependencies need a ring of 3 or more slots");
+  if constexpr (DEP) {
+    if (dep.kt >= 0 && dep.kt <= LEAD) wait_flag(dep.flag, dep.target);
+  }
   issue(0, 0);
   if constexpr (LEAD == 2) {
     issue(min(1, nk - 1), 1);
@@ -386,11 +433,32 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(Params p) {
       if constexpr (LEAD == 2) wait_vmcnt<TILE_INST>();
       else wait_vmcnt<0>();
     }
+    // Group 0 issues k-tile kt + 1 + LEAD right after this barrier and group 1
+    // one phase later: wave 0 holds both at the barrier until the dependency is met.
+    if constexpr (DEP) {
+      if (dep.kt > LEAD && kt == dep.kt - LEAD - 1 && wave == 0) wait_flag(dep.flag, dep.target);
+    }
     if (!(grp == 1 && kt + 1 == nk)) __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   }
   // No DMA may still be writing this workgroup's LDS when it exits.
   wait_vmcnt<0>();
+}
+
+// Stores the accumulators of tile (m0, n0) of batch bz through epilogue EPI.
+// B operand b's accumulators go to columns n0 + b * BOFF + (column within the
+// operand's tile): BOFF = 0 for the epilogues that combine the two operands
+// (SwiGLU), BN when two B operands are two halves of one 2*BN-wide tile.
+template <int BM, int BN, int NB, Epi EPI, int BOFF = 0>
+__device__ __forceinline__ void gemm_epilogue(const Params& p, int m0, int n0, int64_t bz,
+                                              floatx4 (&acc)[NB][WaveTile<BM, BN>::TM][WaveTile<BM, BN>::TN]) {
+  constexpr int WM = WaveTile<BM, BN>::WM, WN = WaveTile<BM, BN>::WN;
+  constexpr int TM = WaveTile<BM, BN>::TM, TN = WaveTile<BM, BN>::TN;
+  constexpr int NOUT = BOFF ? NB : 1;   // B operands stored separately
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
+  const int M = p.m, N = p.n;
 
   // ---- epilogue: lane holds C[row][col .. col+3] for each 16x16 tile
   const int col_in = (lane >> 4) * 4;
@@ -399,6 +467,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(Params p) {
   // that store: z is loaded ZI tile rows at a time (64 VGPRs) before any of
   // those rows is stored.
   constexpr bool kZ = EPI == Epi::kAddZSsqF32 || EPI == Epi::kAddZSsqBf16;
+  static_assert(!(kZ && BOFF), "the residual epilogues store one B operand");
+  static_assert(!(BOFF && (EPI == Epi::kSwiGLU || EPI == Epi::kSwiGLUSplit)), "SwiGLU combines the operands");
   constexpr int ZW = EPI == Epi::kAddZSsqF32 ? 4 : 2;   // 32-bit words of z per lane and tile
   constexpr int ZI = !kZ ? 1 : (64 / (TN * ZW) < TM ? 64 / (TN * ZW) : TM);
   static_assert(TM % ZI == 0, "z batches");
@@ -439,8 +509,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(Params p) {
       if constexpr (EPI == Epi::kRowScale) scale = row_ok ? p.row_scale[gm] : 0.f;
       float ssq = 0.f;
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int gn = n0 + wn * WN + j * 16 + col_in;
+      for (int jj = 0; jj < NOUT * TN; ++jj) {
+        const int bo = jj / TN, j = jj % TN;
+        const int gn = n0 + bo * BOFF + wn * WN + j * 16 + col_in;
         const bool ok = row_ok && gn < N;
         float v[4];
 #pragma unroll
@@ -448,7 +519,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(Params p) {
           if constexpr (EPI == Epi::kSwiGLU || EPI == Epi::kSwiGLUSplit)
             v[r] = silu_f(acc[0][i][j][r]) * acc[NB - 1][i][j][r];
           else
-            v[r] = acc[0][i][j][r] * scale;
+            v[r] = acc[bo][i][j][r] * scale;
           if constexpr (EPI == Epi::kAddZSsqF32) v[r] += __builtin_bit_cast(float, zb[ii][j][r]);
           if constexpr (EPI == Epi::kAddZSsqBf16)
             v[r] += bf16_bits_to_f32(r & 1 ? zb[ii][j][r >> 1] >> 16 : zb[ii][j][r >> 1] & 0xffffu);
@@ -482,6 +553,108 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(Params p) {
           p.part[(int64_t)gm * ((N + WN - 1) / WN) + chunk] = ssq;
       }
     }
+  }
+}
+
+// One BM x BN output tile per workgroup (blockIdx.y = batch), in the
+// XCD-aware tile order.
+template <int BM, int BN, int NB, bool A_KMAJ, Epi EPI, bool KTAIL, int BK, int STAGES, int NSEG>
+__global__ __launch_bounds__(kThreads, 1) void gemm_kernel(Params p) {
+  extern __shared__ __align__(1024) uint8_t smem[];
+  if (p.zero_n && blockIdx.x == 0 && blockIdx.y == 0)
+    for (int i = threadIdx.x; i < p.zero_n; i += kThreads) p.zero[i] = 0;
+  const int tiles_m = (p.m + BM - 1) / BM, tiles_n = (p.n + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(tiles_m, tiles_n, p.group_m, tm, tn);
+  floatx4 acc[NB][WaveTile<BM, BN>::TM][WaveTile<BM, BN>::TN];
+  gemm_mainloop<BM, BN, NB, A_KMAJ, KTAIL, BK, STAGES, NSEG>(p, tm * BM, tn * BN, blockIdx.y, smem, acc);
+  gemm_epilogue<BM, BN, NB, EPI>(p, tm * BM, tn * BN, blockIdx.y, acc);
+}
+
+// ---------------------------------------------------------------- SwiGLU tail + down GEMM
+// After the gate/up launch has produced h[:, :f_main] in full rounds, one launch
+// of 2T equal-work workgroups finishes the operator (T = tail tiles = down tiles):
+//   workgroup i < T:   the gate/up tail tile i (256 x 128, both B operands, full K,
+//                      silu(g)*u into h[:, f_main:]), publishing it per row tile;
+//                      then the first X columns of h times w_down for down tile i,
+//                      whose fp32 accumulators it parks in the workspace.
+//   workgroup T + i:   the remaining F - X columns for down tile i, then adds the
+//                      parked accumulators and stores y (bf16).
+// X balances the two: tail (2*256*128*K flop) + 256*256*X*2 = 256*256*(F - X)*2.
+// The second kind reads h's tail columns only in the last f_tail of its K range,
+// after waiting for the row tile's tail tiles (long finished by then); it waits
+// once more for the parked half.  Producers have the lower workgroup ids, which
+// are dispatched first, so no wait can starve them of a CU.  Down tiles are
+// 256 x 256, run as two B operands of 128 columns (w_down and w_down + 128).
+struct SwigluFused {
+  Params tail;       // x @ (w_gate, w_up)[:, f_main:] -> h[:, f_main:]
+  Params down_a;     // h[:, :X] @ w_down[:X, :]
+  Params down_b;     // h[:, X:] @ w_down[X:, :] -> y
+  floatx4* park;     // [T][waves][2 x TM x TN][64]: down_a's accumulators
+  int* row_done;     // [tiles_m]: tail tiles published per row tile
+  int* park_flag;    // [T]
+  int tail_cols;     // tail tiles per row tile (= down tiles per row tile)
+  int dep_kt;        // first k-tile of down_b that reads h[:, f_main:]
+};
+
+template <int NB, int TM, int TN>
+__device__ __forceinline__ void park_acc(floatx4* tile, const floatx4 (&acc)[NB][TM][TN]) {
+  floatx4* w = tile + (size_t)(threadIdx.x >> 6) * (NB * TM * TN * 64) + (threadIdx.x & 63);
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) w[((b * TM + i) * TN + j) * 64] = acc[b][i][j];
+}
+
+// The parked values are added TN accumulators at a time: the compiler barrier
+// keeps every load from being hoisted ahead of the adds, which would hold the
+// parked tile and the accumulators (2 x 128 VGPRs) at once and spill.
+template <int NB, int TM, int TN>
+__device__ __forceinline__ void add_parked(const floatx4* tile, floatx4 (&acc)[NB][TM][TN]) {
+  const floatx4* w = tile + (size_t)(threadIdx.x >> 6) * (NB * TM * TN * 64) + (threadIdx.x & 63);
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        acc[b][i][j] += w[((b * TM + i) * TN + j) * 64];
+        asm volatile("" : "+v"(acc[b][i][j]) :: "memory");   // the sum exists before the next batch
+      }
+    }
+}
+
+__global__ __launch_bounds__(kThreads, 1) void swiglu_tail_down_kernel(SwigluFused f) {
+  constexpr int BM = 256, BN = 128, NB = 2;
+  using W = WaveTile<BM, BN>;
+  extern __shared__ __align__(1024) uint8_t smem[];
+  floatx4 acc[NB][W::TM][W::TN];
+  const int tiles_m = (f.tail.m + BM - 1) / BM;
+  const int T = tiles_m * f.tail_cols;
+  const bool producer = (int)blockIdx.x < T;
+  const int i = producer ? (int)blockIdx.x : (int)blockIdx.x - T;
+  // tile i: column tile i % tail_cols of row tile i / tail_cols; workgroups i and
+  // T + i sit on the same XCD (T is a multiple of 8), each XCD holding two column
+  // tiles of every row tile
+  const int tm = i / f.tail_cols, tc = i % f.tail_cols;
+  constexpr size_t kParkTile = (size_t)kWaves * NB * W::TM * W::TN * 64;   // floatx4 per tile
+  if (producer) {
+    gemm_mainloop<BM, BN, NB, true, false, kBK, kStages, 1>(f.tail, tm * BM, tc * BN, 0, smem, acc);
+    gemm_epilogue<BM, BN, NB, Epi::kSwiGLU>(f.tail, tm * BM, tc * BN, 0, acc);
+    publish(&f.row_done[tm]);   // its barrier also ends this workgroup's LDS reads
+    gemm_mainloop<BM, BN, NB, true, false, kBK, kStages, 1>(f.down_a, tm * BM, tc * 2 * BN, 0, smem, acc);
+    park_acc(f.park + (size_t)i * kParkTile, acc);
+    publish(&f.park_flag[i]);
+  } else {
+    const KDep dep{f.dep_kt, &f.row_done[tm], f.tail_cols};
+    gemm_mainloop<BM, BN, NB, true, false, kBK, kStages, 1, true>(f.down_b, tm * BM, tc * 2 * BN, 0, smem,
+                                                                 acc, dep);
+    if (threadIdx.x < 64) wait_flag(&f.park_flag[i], 1);
+    __syncthreads();
+    add_parked(f.park + (size_t)i * kParkTile, acc);
+    gemm_epilogue<BM, BN, NB, Epi::kStore, BN>(f.down_b, tm * BM, tc * 2 * BN, 0, acc);
   }
 }
 
@@ -1425,6 +1598,46 @@ extern "C" int kda_swiglu_bf16(const kda_bf16* x, const kda_bf16* w_up, const kd
   const UpSplit us = plan_up(m, f);
   Params up = make_params(m, us.f_main, h, f);
   add_seg(up, x, k, w_gate, f, k, w_up);
+  // The gate/up tail and the down GEMM in one launch of equal-work workgroups
+  // (swiglu_tail_down_kernel) when the tail's 256x128 tiles pair one to one with
+  // the down GEMM's 256x256 tiles and both kinds fit one round over the device
+  // (2048 x 4096 -> 14336: 128 + 128 workgroups on 256 CUs).
+  {
+    const int64_t tiles_m = (m + 255) / 256;
+    const int64_t t = tiles_m * (k / 256);
+    const int64_t x_split = (f - k) / 2 / kBK * kBK;   // down columns done by the tail workgroups
+    const SizeTerm park_n = SizeTerm(t) * (int64_t)(kWaves * 2 * 8 * 2 * 64);
+    Carve cv{reinterpret_cast<uint8_t*>(workspace)};
+    floatx4* park = cv.take<floatx4>(park_n);
+    int* flags = cv.take<int>(tiles_m + t);
+    if (have_ws && us.f_tail > 0 && k % 256 == 0 && us.f_tail == 128 * (k / 256) && t % kXcds == 0 &&
+        2 * t <= device_cu_count() && f % kBK == 0 && x_split >= kBK && us.f_main - x_split >= 4 * kBK &&
+        cv.used >= 0 && cv.used <= workspace_bytes_) {
+      static const bool attr_ok =
+          hipFuncSetAttribute(reinterpret_cast<const void*>(swiglu_tail_down_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kStages * 4 * kBK * 128 * 2) ==
+          hipSuccess;
+      if (!attr_ok) return set_error(KDA_ERR_HIP, "swiglu_bf16: cannot reserve LDS for the tail/down launch");
+      up.zero = flags;                  // the flags below start at zero
+      up.zero_n = (int)(tiles_m + t);
+      if (int rc = launch<256, 128, 2, true, Epi::kSwiGLU>(up, 1, st, "swiglu_bf16(up/gate)")) return rc;
+      SwigluFused fz{};
+      fz.tail = make_params(m, us.f_tail, h + us.f_main, f);
+      add_seg(fz.tail, x, k, w_gate + us.f_main, f, k, w_up + us.f_main);
+      fz.down_a = make_params(m, k, y, k);
+      add_seg(fz.down_a, h, f, w_down, k, x_split, w_down + 128);
+      fz.down_b = make_params(m, k, y, k);
+      add_seg(fz.down_b, h + x_split, f, w_down + x_split * k, k, f - x_split, w_down + x_split * k + 128);
+      fz.park = park;
+      fz.row_done = flags;
+      fz.park_flag = flags + tiles_m;
+      fz.tail_cols = (int)(k / 256);
+      fz.dep_kt = (int)((us.f_main - x_split) / kBK);
+      hipLaunchKernelGGL(swiglu_tail_down_kernel, dim3((unsigned)(2 * t)), dim3(kThreads),
+                         kStages * 4 * kBK * 128 * 2, st, fz);
+      return check_launch("swiglu_bf16(tail + down)");
+    }
+  }
   if (int rc = launch<256, 128, 2, true, Epi::kSwiGLU>(up, 1, st, "swiglu_bf16(up/gate)")) return rc;
   if (us.f_tail > 0) {
     Params t = make_params(m, us.f_tail, h + us.f_main, f);

@@ -191,6 +191,31 @@ def test_swiglu_split_k_ragged_rows_dirty_workspace(dev):
     assert torch.equal(first, second)
 
 
+def test_swiglu_tail_down_launch_ragged_rows_dirty_workspace(dev):
+    # M = 300, K = 1024, F = 16896: 264 gate/up tiles of 256x128 on 256 CUs, so the
+    # last 512 columns (8 tiles, 4 per row tile) run in one launch with the down
+    # GEMM's 8 tiles of 256x256: 8 workgroups compute a tail tile and then h's
+    # first 7936 columns times w_down, parking the fp32 sums; 8 more compute the
+    # remaining 8960 columns, waiting for the tail tiles of their row before its
+    # last 512 columns and for the parked sums before the epilogue.  The second
+    # row tile holds 44 rows.  The workspace starts as 0xff bytes (the flags are
+    # cleared by the gate/up launch), a second call gives the same bits, and the
+    # result matches the path without a workspace within one bf16 rounding.
+    m, k, f = 300, 1024, 16896
+    d = oi.draw("swiglu_cfg", 4, dims=dict(M=m, K=k, F=f))
+    args = [to_dev(d[n], dev, BF) for n in ("x", "w_up", "w_down", "w_gate")]
+    ws = torch.full((ops.workspace_size(_lib.OP_SWIGLU_BF16, 1, m, k, f),), 255,
+                    dtype=torch.uint8, device=dev)
+    first = ops.swiglu(*args, workspace=ws)
+    second = ops.swiglu(*args, workspace=ws)
+    unsplit = ops.swiglu(*args, workspace=torch.empty(16, dtype=torch.uint8, device=dev))
+    err = rel_l2(to_host(first), oo.swiglu(**d))
+    print(f"swiglu tail+down M={m} K={k} F={f} rel_l2={err:.3e}", flush=True)
+    assert err < 5e-3
+    assert torch.equal(first, second)
+    assert rel_l2(to_host(first), to_host(unsplit)) < 2.0 ** -8
+
+
 @pytest.mark.parametrize("dims", [dict(M=256, K=128, F=64), dict(M=50, K=96, F=200),
                                   dict(M=300, K=264, F=136)])
 def test_swiglu_ragged(dev, dims):
