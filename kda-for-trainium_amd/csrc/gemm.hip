@@ -691,7 +691,8 @@ __global__ __launch_bounds__(kSkThreads, 4) void bmm_smallk_kernel(const float* 
                                                                 const float* __restrict__ b,
                                                                 float* __restrict__ c, int m,
                                                                 int n, int k, int tiles_n) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // scalar
   const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
   const int64_t bz = blockIdx.y;
   const int m0 = tm * kSkTile + (wave >> 1) * kSkWave;
@@ -737,24 +738,31 @@ __global__ __launch_bounds__(kSkThreads, 4) void bmm_smallk_kernel(const float* 
   // 4 rows x 256 contiguous bytes (measured 5.9 TB/s against 3.4 TB/s).  Each wave
   // uses its own 16 x 68-float buffer (rows padded by 4 floats: conflict-free for
   // both the writes and the reads); no barrier is needed within a wave.
+  // The lane index is derived again from the exec mask (mbcnt) rather than kept
+  // in a register across the K loop: at 4 waves per SIMD (128 VGPRs) that one
+  // register was spilled, and a kernel with scratch is dispatched more slowly.
   __shared__ __align__(16) float stage[4][16][kSkWave + 4];
   float (*buf)[kSkWave + 4] = stage[wave];
+  {
+    const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    const int l16e = lane_e & 15, ge = lane_e >> 4;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      *reinterpret_cast<floatx4*>(&buf[l16][16 * j + 4 * g]) = acc[i][j];
+      *reinterpret_cast<floatx4*>(&buf[l16e][16 * j + 4 * ge]) = acc[i][j];
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int r = 4 * q + g;               // row within the block
-      const floatx4 v = *reinterpret_cast<const floatx4*>(&buf[r][4 * l16]);
+      const int r = 4 * q + ge;              // row within the block
+      const floatx4 v = *reinterpret_cast<const floatx4*>(&buf[r][4 * l16e]);
       const int row = m0 + 16 * i + r;
-      const int col = n0 + 4 * l16;
+      const int col = n0 + 4 * l16e;
       if (row < m && col < n)
         __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(cb + (int64_t)row * n + col));
     }
     __builtin_amdgcn_wave_barrier();
+  }
   }
 }
 
