@@ -96,9 +96,10 @@ enum {
 };
 
 /* Workspace bytes for operator `op` at the given sizes (unused sizes: 0);
- * -1 for an unknown op, a negative size, or sizes whose three largest multiply
- * to more than 2^40 elements (beyond any device).  The sizes depend only on the
- * arguments, not on the device. */
+ * -1 for an unknown op, a negative size, or sizes whose workspace does not fit
+ * in int64 (every product and sum is overflow-checked); entry points refuse such
+ * sizes with KDA_ERR_UNSUPPORTED.  The sizes depend only on the arguments, not on
+ * the device. */
 int64_t kda_workspace_size(int op, int64_t batch, int64_t m, int64_t k, int64_t n, int64_t r);
 
 /* ---------------------------------------------------------------- bf16 GEMMs

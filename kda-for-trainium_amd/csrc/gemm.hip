@@ -866,6 +866,13 @@ __global__ __launch_bounds__(256) void split_transpose_f32_kernel(const float* _
   }
 }
 
+// Zeroes n 16-bit words: the output of a product whose inner dimension is 0.
+// A kernel rather than a memset, so a caller may capture the call in a graph.
+__global__ __launch_bounds__(256) void zero_u16_kernel(uint16_t* __restrict__ y, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    y[i] = 0;
+}
+
 // Sum of the two fp32 split-K partials [2][n] into bf16 (n % 4 == 0).
 __global__ __launch_bounds__(256) void splitk2_bf16_kernel(const floatx4* __restrict__ part,
                                                            u32x2* __restrict__ y, int64_t n4) {
@@ -1215,7 +1222,8 @@ int validate(const char* what, const void* a, const void* b, const void* c, int6
     return set_error(KDA_ERR_UNSUPPORTED,
                      "%s: K (%lld) and N (%lld) must be multiples of 8 (16-byte rows)", what,
                      (long long)k, (long long)n);
-  if (m && n && (!a || !b || !c)) return set_error(KDA_ERR_INVALID_ARG, "%s: null pointer", what);
+  // a and b hold no element when K = 0 (empty tensors may have null data)
+  if (m && n && (!c || (k && (!a || !b)))) return set_error(KDA_ERR_INVALID_ARG, "%s: null pointer", what);
   if (!aligned16(a) || !aligned16(b) || !aligned16(c))
     return set_error(KDA_ERR_INVALID_ARG, "%s: pointers must be 16-byte aligned", what);
   return KDA_OK;
@@ -1416,6 +1424,14 @@ int check_split_k(const char* what, int64_t k) {
   return KDA_OK;
 }
 
+// Zero `bytes` bytes (a multiple of 2) of a kernel output on `st`.
+int zero_output(void* y, int64_t bytes, hipStream_t st, const char* what) {
+  const int64_t n = bytes / 2;
+  const unsigned blocks = (unsigned)(n / 256 + 1 < 2048 ? n / 256 + 1 : 2048);
+  hipLaunchKernelGGL(zero_u16_kernel, dim3(blocks), dim3(256), 0, st, reinterpret_cast<uint16_t*>(y), n);
+  return check_launch(what);
+}
+
 }  // namespace gemm
 }  // namespace kda
 
@@ -1435,8 +1451,7 @@ extern "C" int kda_matmul_bf16(const kda_bf16* a, const kda_bf16* b, kda_bf16* c
   clear_error();
   if (int rc = validate("matmul_bf16", a, b, c, m, n, k)) return rc;
   if (m == 0 || n == 0) return KDA_OK;
-  if (k == 0) return hipMemsetAsync(c, 0, (size_t)m * n * 2, as_stream(stream)) == hipSuccess
-                         ? KDA_OK : set_error(KDA_ERR_HIP, "matmul_bf16: memset failed");
+  if (k == 0) return zero_output(c, (int64_t)m * n * 2, as_stream(stream), "matmul_bf16");
   Params p = make_params(m, n, c, n);
   add_seg(p, a, k, b, n, k);
   return launch_auto<true, Epi::kStore>(p, 1, as_stream(stream), "matmul_bf16");
@@ -1591,11 +1606,10 @@ extern "C" int kda_swiglu_bf16(const kda_bf16* x, const kda_bf16* w_up, const kd
   clear_error();
   if (int rc = validate("swiglu_bf16(up/gate)", x, w_gate, h, m, f, k)) return rc;
   if (int rc = validate("swiglu_bf16(down)", h, w_down, y, m, k, f)) return rc;
-  if (!w_up || !aligned16(w_up))
+  if (!aligned16(w_up) || (k && f && !w_up))
     return set_error(KDA_ERR_INVALID_ARG, "swiglu_bf16: w_up null or misaligned");
   if (m == 0 || k == 0) return KDA_OK;
-  if (f == 0) return hipMemsetAsync(y, 0, (size_t)m * k * 2, as_stream(stream)) == hipSuccess
-                         ? KDA_OK : set_error(KDA_ERR_HIP, "swiglu_bf16: memset failed");
+  if (f == 0) return zero_output(y, (int64_t)m * k * 2, as_stream(stream), "swiglu_bf16");
   hipStream_t st = as_stream(stream);
   const int64_t ws_need = workspace_bytes(KDA_OP_SWIGLU_BF16, 1, m, k, f, 0);
   const bool have_ws = workspace && aligned16(workspace) && ws_need >= 0 && workspace_bytes_ >= ws_need;
@@ -1696,8 +1710,7 @@ extern "C" int kda_matmul_f32(const float* lhs, const float* rhs, float* out, in
   if (int rc = validate(what, lhs, rhs, out, m, n, k)) return rc;
   if (int rc = check_split_k(what, k)) return rc;
   if (m == 0 || n == 0) return KDA_OK;
-  if (k == 0) return hipMemsetAsync(out, 0, (size_t)m * n * 4, as_stream(stream)) == hipSuccess
-                         ? KDA_OK : set_error(KDA_ERR_HIP, "%s: memset failed", what);
+  if (k == 0) return zero_output(out, (int64_t)m * n * 4, as_stream(stream), what);
   if (int rc = check_ws(what, workspace, ws_bytes, workspace_bytes(KDA_OP_MATMUL_F32, 1, m, k, n, 0)))
     return rc;
   hipStream_t st = as_stream(stream);
@@ -1723,8 +1736,7 @@ extern "C" int kda_transpose_matmul_f32(const float* lhs, const float* rhs, floa
   if (int rc = check_split_k(what, k)) return rc;
   if (m % 8) return set_error(KDA_ERR_UNSUPPORTED, "%s: M (%lld) must be a multiple of 8", what, (long long)m);
   if (m == 0 || n == 0) return KDA_OK;
-  if (k == 0) return hipMemsetAsync(out, 0, (size_t)m * n * 4, as_stream(stream)) == hipSuccess
-                         ? KDA_OK : set_error(KDA_ERR_HIP, "%s: memset failed", what);
+  if (k == 0) return zero_output(out, (int64_t)m * n * 4, as_stream(stream), what);
   if (int rc = check_ws(what, workspace, ws_bytes,
                         workspace_bytes(KDA_OP_TRANSPOSE_MATMUL_F32, 1, m, k, n, 0)))
     return rc;
@@ -1756,8 +1768,7 @@ extern "C" int kda_bmm_f32(const float* lhs, const float* rhs, float* out, int64
   if (int rc = validate(what, lhs, rhs, out, m, n, k)) return rc;
   if (int rc = check_split_k(what, k)) return rc;
   if (batch == 0 || m == 0 || n == 0) return KDA_OK;
-  if (k == 0) return hipMemsetAsync(out, 0, (size_t)batch * m * n * 4, as_stream(stream)) == hipSuccess
-                         ? KDA_OK : set_error(KDA_ERR_HIP, "%s: memset failed", what);
+  if (k == 0) return zero_output(out, (int64_t)batch * m * n * 4, as_stream(stream), what);
   hipStream_t st = as_stream(stream);
   if (k <= kSmallKMax) {
     // output-bound: fragments split in registers, no workspace needed
@@ -1798,8 +1809,9 @@ extern "C" int kda_lora_f32(const float* x, const float* w, const float* a, cons
   if (int rc = validate(what, x, a, out, m, r, k)) return rc;
   if (int rc = check_split_k(what, k)) return rc;
   if (int rc = check_split_k(what, r)) return rc;
-  if (!b || !aligned16(b)) return set_error(KDA_ERR_INVALID_ARG, "%s: b null or misaligned", what);
+  if (!aligned16(b) || (r && n && !b)) return set_error(KDA_ERR_INVALID_ARG, "%s: b null or misaligned", what);
   if (m == 0 || n == 0) return KDA_OK;
+  if (k == 0) return zero_output(out, (int64_t)m * n * 4, as_stream(stream), what);   // x@w = x@a = 0
   if (int rc = check_ws(what, workspace, ws_bytes, workspace_bytes(KDA_OP_LORA_F32, 1, m, k, n, r)))
     return rc;
   hipStream_t st = as_stream(stream);
@@ -1843,8 +1855,6 @@ extern "C" int kda_lora_f32(const float* x, const float* w, const float* a, cons
   Params p = make_params(m, n, out, n);
   add_split_segs(p, lp.xw.ah, lp.xw.al, k, lp.xw.bh, lp.xw.bl, n, k);
   if (r > 0) add_split_segs(p, lp.th, lp.tl, r, lp.bh, lp.bl, n, r);
-  if (p.k == 0) return hipMemsetAsync(out, 0, (size_t)m * n * 4, st) == hipSuccess
-                           ? KDA_OK : set_error(KDA_ERR_HIP, "%s: memset failed", what);
   return launch_auto<true, Epi::kStoreF32>(p, 1, st, what);
 }
 
@@ -1946,10 +1956,10 @@ extern "C" int kda_swiglu_f32(const float* x, const float* w_up, const float* w_
   if (int rc = validate(what, x, w_down, out, m, k, f)) return rc;
   if (int rc = check_split_k(what, k)) return rc;
   if (int rc = check_split_k(what, f)) return rc;
-  if (!w_up || !aligned16(w_up)) return set_error(KDA_ERR_INVALID_ARG, "%s: w_up null or misaligned", what);
+  if (!aligned16(w_up) || (k && f && !w_up))
+    return set_error(KDA_ERR_INVALID_ARG, "%s: w_up null or misaligned", what);
   if (m == 0 || k == 0) return KDA_OK;
-  if (f == 0) return hipMemsetAsync(out, 0, (size_t)m * k * 4, as_stream(stream)) == hipSuccess
-                         ? KDA_OK : set_error(KDA_ERR_HIP, "%s: memset failed", what);
+  if (f == 0) return zero_output(out, (int64_t)m * k * 4, as_stream(stream), what);
   if (int rc = check_ws(what, workspace, ws_bytes, workspace_bytes(KDA_OP_SWIGLU_F32, 1, m, k, f, 0)))
     return rc;
   hipStream_t st = as_stream(stream);
