@@ -766,6 +766,165 @@ __global__ __launch_bounds__(kSkThreads, 4) void bmm_smallk_kernel(const float* 
   }
 }
 
+// Persistent form of the small-K bmm for K = 64 and whole 128 x 128 tiles: two
+// workgroups per CU each loop over tiles, and the stores of one tile stay in
+// flight while the operands of the next arrive and are multiplied.  vmcnt
+// counts loads and stores together and retires them in issue order, so a wave
+// issues the operand DMAs of tile t+1 before the 16 stores of tile t, and at the
+// top of the next iteration waits with vmcnt(16): the DMAs are done, the stores
+// need not be.  The operands go straight from global memory into LDS (no
+// registers held across the stores): A as 128 rows x 256 bytes (16-byte chunk c
+// of row r at position c ^ (r & 15)), B as 64 k-rows x 512 bytes (chunk c of
+// k-row r at position (c - 4 * ((r >> 3) & 3)) mod 32), both conflict-free for
+// the fragment reads.  After the MFMAs the 64 KiB is reused to transpose the
+// accumulators into 4-row x 256-byte store pieces, as in bmm_smallk_kernel
+// (wave w's 64 x 64 block at 16 KiB * w, chunk c of row r at position c ^ (r & 15)).
+constexpr int kPkTile = 128;                       // C tile per workgroup
+constexpr int kPkK = 64;                           // the only K it takes
+constexpr int kPkABytes = kPkTile * kPkK * 4;      // 32 KiB
+constexpr int kPkBBytes = kPkK * kPkTile * 4;      // 32 KiB
+constexpr int kPkDmaPerWave = (kPkABytes + kPkBBytes) / 1024 / 4;   // 16
+constexpr int kPkStores = 16;                      // 64 x 64 fp32 per wave, 1 KiB per store
+constexpr int kPkWgPerCu = 2;
+
+// B k-row r's chunk rotation (a multiple of 4 chunks = 16 banks per 8-row group).
+__host__ __device__ __forceinline__ int pk_brot(int r) { return 4 * ((r >> 3) & 3); }
+
+// Tile t of the batched grid: (batch, row block, column block), column blocks fastest.
+struct PkTile {
+  int64_t bz;
+  int tm, tn;
+};
+__host__ __device__ __forceinline__ PkTile pk_tile(int64_t t, int tiles_m, int tiles_n) {
+  const int64_t per_b = (int64_t)tiles_m * tiles_n;
+  const int r = (int)(t % per_b);
+  return PkTile{t / per_b, r / tiles_n, r % tiles_n};
+}
+// Byte offsets, from the tile's first A row / first B element, of the 16 bytes
+// that lane `lane` of DMA instruction `inst` (0..31 for A, 0..31 for B) fetches.
+__host__ __device__ __forceinline__ uint32_t pk_a_off(int inst, int lane) {
+  const int row = inst * 4 + (lane >> 4);
+  return (uint32_t)(row * (kPkK * 4) + (((lane & 15) ^ (row & 15)) << 4));
+}
+__host__ __device__ __forceinline__ uint32_t pk_b_off(int inst, int lane, int n) {
+  const int row = inst * 2 + (lane >> 5);
+  return (uint32_t)row * (uint32_t)n * 4u + (uint32_t)((((lane & 31) + pk_brot(row)) & 31) << 4);
+}
+
+// split8 with one conversion per pair of hi values: the same limbs, fewer VALU
+// instructions (this kernel has the registers for it).
+__device__ __forceinline__ void split8_pairs(const float (&x)[8], bf16x8& hi, bf16x8& lo) {
+  u32x4 h, l;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    uint32_t he, le;
+    split_bf16x2(x[2 * e], x[2 * e + 1], he, le);
+    h[e] = he;
+    l[e] = le;
+  }
+  hi = __builtin_bit_cast(bf16x8, h);
+  lo = __builtin_bit_cast(bf16x8, l);
+}
+
+__global__ __launch_bounds__(kSkThreads, kPkWgPerCu) void bmm_smallk_persist_kernel(
+    const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ c, int m, int n,
+    int tiles_m, int tiles_n, int64_t tiles) {
+  __shared__ __align__(1024) uint8_t lds[kPkABytes + kPkBBytes];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l16 = lane & 15, g = lane >> 4;
+  const int wr = 64 * (wave >> 1), wc = 64 * (wave & 1);   // the wave's 64 x 64 block in the tile
+
+  auto issue = [&](int64_t t) {
+    const PkTile pt = pk_tile(t, tiles_m, tiles_n);
+    const float* as = a + (pt.bz * m + (int64_t)pt.tm * kPkTile) * kPkK;
+    const float* bs = b + pt.bz * kPkK * (int64_t)n + (int64_t)pt.tn * kPkTile;
+#pragma unroll
+    for (int q = 0; q < kPkDmaPerWave / 2; ++q) {
+      const int inst = 4 * q + wave;
+      dma16(as, pk_a_off(inst, lane), lds_addr(lds + inst * 1024));
+    }
+#pragma unroll
+    for (int q = 0; q < kPkDmaPerWave / 2; ++q) {
+      const int inst = 4 * q + wave;
+      dma16(bs, pk_b_off(inst, lane, n), lds_addr(lds + kPkABytes + inst * 1024));
+    }
+  };
+
+  int64_t t = blockIdx.x;
+  issue(t);
+  wait_vmcnt<0>();
+  for (;;) {
+    __builtin_amdgcn_s_barrier();   // every wave's DMAs of tile t have landed
+    asm volatile("" ::: "memory");
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8 bh[4], bl[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int cb = wc + 16 * j + l16;
+        const int pos = ((cb >> 2) - pk_brot(32 * ks + 8 * g)) & 31;
+        const uint8_t* src = lds + kPkABytes + (32 * ks + 8 * g) * (kPkTile * 4) + (pos << 4) + 4 * (cb & 3);
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = *reinterpret_cast<const float*>(src + e * (kPkTile * 4));
+        split8_pairs(x, bh[j], bl[j]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ra = wr + 16 * i + l16;
+        const int pos = (8 * ks + 2 * g) ^ l16;
+        const uint8_t* row = lds + ra * (kPkK * 4);
+        const floatx4 v0 = *reinterpret_cast<const floatx4*>(row + (pos << 4));
+        const floatx4 v1 = *reinterpret_cast<const floatx4*>(row + ((pos ^ 1) << 4));
+        const float x[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        bf16x8 ah, al;
+        split8_pairs(x, ah, al);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh[j], ah, acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bl[j], ah, acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh[j], al, acc[i][j], 0, 0, 0);
+        }
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();   // every wave is done reading the operands
+    asm volatile("" ::: "memory");
+    uint8_t* stage = lds + wave * 16384;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<floatx4*>(stage + (16 * i + l16) * 256 + (((4 * j + g) ^ l16) << 4)) = acc[i][j];
+    __builtin_amdgcn_wave_barrier();
+    floatx4 v[kPkStores];
+#pragma unroll
+    for (int q = 0; q < kPkStores; ++q) {
+      const int r = 4 * q + g;   // rows 16i + 4qq + g, q = 4i + qq
+      v[q] = *reinterpret_cast<const floatx4*>(stage + r * 256 + ((l16 ^ (r & 15)) << 4));
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();   // every wave holds its tile: the LDS is free
+    asm volatile("" ::: "memory");
+    const PkTile pt = pk_tile(t, tiles_m, tiles_n);
+    const int64_t next = t + gridDim.x;
+    if (next < tiles) issue(next);
+    float* cb = c + (pt.bz * m + (int64_t)pt.tm * kPkTile + wr) * n + (int64_t)pt.tn * kPkTile + wc + 4 * l16;
+#pragma unroll
+    for (int q = 0; q < kPkStores; ++q)
+      __builtin_nontemporal_store(v[q], reinterpret_cast<floatx4*>(cb + (int64_t)(4 * q + g) * n));
+    if (next >= tiles) break;
+    t = next;
+    wait_vmcnt<kPkStores>();   // the DMAs of tile `next`; this tile's stores may stay in flight
+  }
+}
+
 // ---------------------------------------------------------------- pre-passes
 
 // Up to kMaxSplitJobs fp32 arrays, each split into (hi, lo) bf16 planes in one
@@ -1778,6 +1937,14 @@ extern "C" int kda_bmm_f32(const float* lhs, const float* rhs, float* out, int64
     const int64_t tiles = ((m + kSkTile - 1) / kSkTile) * (int64_t)tiles_n;
     if (tiles > 0x7fffffff || batch > 65535)
       return set_error(KDA_ERR_UNSUPPORTED, "%s: problem too large", what);
+    if (k == kPkK && m % kPkTile == 0 && n % kPkTile == 0 && n <= (1 << 24) && aligned16(rhs)) {
+      // whole tiles: the persistent form (its 32-bit B DMA offsets reach 63 * N * 4 + 512 bytes)
+      const int64_t all = tiles * batch;
+      const int64_t grid = std::min<int64_t>(all, (int64_t)kPkWgPerCu * device_cu_count());
+      hipLaunchKernelGGL(bmm_smallk_persist_kernel, dim3((unsigned)grid), dim3(kSkThreads), 0, st, lhs,
+                         rhs, out, (int)m, (int)n, (int)(m / kPkTile), tiles_n, all);
+      return check_launch(what);
+    }
     hipLaunchKernelGGL(bmm_smallk_kernel, dim3((unsigned)tiles, (unsigned)batch), dim3(kSkThreads),
                        0, st, lhs, rhs, out, (int)m, (int)n, (int)k, tiles_n);
     return check_launch(what);

@@ -99,9 +99,27 @@ def test_bmm_full_size_every_batch():
 
 
 @pytest.mark.parametrize("dims", [dict(B=3, M=256, K=64, N=256), dict(B=2, M=100, K=96, N=72),
-                                  dict(B=2, M=130, K=32, N=200), dict(B=1, M=17, K=64, N=8)])
+                                  dict(B=2, M=130, K=32, N=200), dict(B=1, M=17, K=64, N=8),
+                                  dict(B=7, M=2048, K=64, N=1280), dict(B=16, M=256, K=64, N=2048),
+                                  dict(B=20, M=128, K=64, N=4096)])
 def test_bmm_small(dims):
+    # K = 64 with M and N multiples of 128 runs the persistent kernel: 1120, 512 and
+    # 640 tiles (several per workgroup, uneven counts)
     assert _run("bmm", ops.bmm, oo.bmm, 5, dims=dims) < GATE
+
+
+def test_bmm_persistent_matches_per_tile_kernel():
+    """The persistent kernel (whole 128 x 128 tiles, K = 64) and the per-tile kernel
+    (taken when N is not a multiple of 128) do the same arithmetic in the same
+    order: widening rhs by 8 columns leaves the first 2048 columns bit-identical."""
+    d = oi.draw("bmm", 3, dims=dict(B=16, M=384, K=64, N=2048))
+    lhs, rhs = to_dev(d["lhs"], "cuda"), to_dev(d["rhs"], "cuda")
+    wide = torch.cat([rhs, torch.randn(16, 64, 8, device="cuda")], dim=2).contiguous()
+    a = ops.bmm(lhs, rhs)
+    b = ops.bmm(lhs, wide)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b[:, :, :2048])
+    assert rel_l2(to_host(a), oo.bmm(d["lhs"], d["rhs"])) < GATE
 
 
 @pytest.mark.parametrize("dims", [dict(B=2, M=130, K=64, N=200), dict(B=3, M=64, K=32, N=72)])
