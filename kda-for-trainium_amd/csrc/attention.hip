@@ -8,7 +8,10 @@
 // block of 256 / HPW queries), HPW the largest power of two up to 8 dividing G;
 // its 8 waves are the HPW heads x 8 / HPW blocks of 32 query rows, so each K/V
 // tile staged in LDS is read by HPW query heads (the graded G = 4: 4 heads x 64
-// queries).  Causal blocks with the most key tiles are scheduled first.
+// queries).  Causal blocks with the most key tiles are scheduled first, on a
+// persistent grid of one workgroup per CU that runs its blocks in a snake over
+// that order (even totals); a block's last iterations prefetch the next block's
+// first K/V tiles.
 //
 // Staging: K and V tiles of 64 keys go straight from global memory into LDS
 // (global_load_lds_dwordx4, no register staging), each through a 4-slot ring
@@ -44,6 +47,8 @@
 //   The second wave of each SIMD
 //   runs at a raised issue priority so both reach the per-iteration barrier
 //   together.
+#include <algorithm>
+
 #include "attention_geom.h"
 #include "common.h"
 #include "lanes.h"
@@ -57,7 +62,6 @@ namespace attn {
 constexpr int kIT = kWaveRows / 16;
 constexpr int kDT = kD / 16;                                // O^T tiles along d
 constexpr float kLazy = 8.0f;  // running-max slack (log2 units) before O is rescaled
-constexpr int kRing = 4;       // K and V tile slots in LDS (a power of two: slot = kt & 3)
 
 typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -296,15 +300,62 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   const int l16 = lane & 15;
   const int g = lane >> 4;
 
-  // (batch, kv head, query head, rows) of this workgroup and wave; causal
-  // blocks with the most key tiles first
-  const Block blk = block_of(p, CAUSAL, HPW, (int)blockIdx.x, wave);
-  const int w0 = blk.w0;                            // this wave's first query row
-
   // The instruction arbiter serves the older waves (0-3) of each SIMD first, and
   // they also issue the K/V DMAs; the younger waves get a higher issue priority
   // so both reach the per-iteration barrier together (1.3 % same-box).
   if (__builtin_amdgcn_readfirstlane(wave) >= kDmaWaves) __builtin_amdgcn_s_setprio(1);
+
+  // ---- DMA geometry: instruction j of issuing wave w (< kDmaWaves) fills LDS
+  // bytes [(j*kDmaWaves + w)*1024, +1024) of a tile = rows 4q .. 4q+3, lane -> (row, chunk).
+  // Per-lane byte offsets within a tile (row * row_bytes + swizzled chunk) are
+  // the same for every block; the LDS destination of each instruction is wave-uniform.
+  const int64_t row_bytes = p.k_ss * 2;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  uint32_t koff[kDmaPerWave], voff[kDmaPerWave];
+#pragma unroll
+  for (int j = 0; j < kDmaPerWave; ++j) {
+    const int r = dma_row(j, wave, lane);
+    koff[j] = dma_lane_offset(row_bytes, r, dma_kcol(r, lane));
+    voff[j] = dma_lane_offset(row_bytes, r, dma_vcol(r, lane));
+  }
+  // Rows past the sequence (only in the last, partial tile) are clamped to the
+  // last key: their scores are masked and their V rows meet p = 0.
+  auto issue = [&](const char* base, bool is_v, const uint32_t (&off)[kDmaPerWave], int kt,
+                   uint32_t lds) {
+    if (wave_u >= kDmaWaves) return;
+    const int j0 = kt * kBN;
+    const char* tb = base + (int64_t)j0 * row_bytes;
+    if (j0 + kBN <= p.seq) {
+#pragma unroll
+      for (int j = 0; j < kDmaPerWave; ++j)
+        dma16(tb, off[j], lds + (uint32_t)((j * kDmaWaves + wave_u) * 1024));
+    } else {
+#pragma unroll
+      for (int j = 0; j < kDmaPerWave; ++j) {
+        const int r = dma_row(j, wave, lane);
+        dma16(tb, dma_lane_offset(row_bytes, dma_src_row(p, kt, r), is_v ? dma_vcol(r, lane) : dma_kcol(r, lane)),
+              lds + (uint32_t)((j * kDmaWaves + wave_u) * 1024));
+      }
+    }
+  };
+
+  // Causal: persistent, this workgroup's blocks (sched_block), each (batch, kv
+  // head, query heads, rows), longest first.  The last iterations of a block
+  // prefetch the next block's first K/V tiles into the ring slots that follow its
+  // own (ring_slot), so the next block starts without waiting for them.
+  // Non-causal blocks are all equally long: one block per workgroup (the loop
+  // runs once, and the compiler sees it).
+  const int nb_total = total_blocks(p, HPW);
+  int slot_base = 0;   // ring position of the current block's first tile
+  int prev_nkt = 0;    // tile count of the previous block (0: none)
+  for (int kk = 0; CAUSAL || kk == 0; ++kk) {
+  const int bid = sched_block(kk, (int)blockIdx.x, (int)gridDim.x);
+  if (bid >= nb_total) break;
+  if (kk > 0) __syncthreads();   // every wave is done with the previous block's LDS
+  const Block blk = block_of(p, CAUSAL, HPW, bid, wave);
+  const int bid_next = sched_block(kk + 1, (int)blockIdx.x, (int)gridDim.x);
+  const int w0 = blk.w0;                            // this wave's first query row
+
   State st;
   {
     // Q fragments, scaled by scale*log2(e) and rounded to bf16 once
@@ -334,43 +385,10 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
     }
   }
 
-  // ---- DMA geometry: instruction j of issuing wave w (< kDmaWaves) fills LDS
-  // bytes [(j*kDmaWaves + w)*1024, +1024) of a tile = rows 4q .. 4q+3, lane -> (row, chunk)
-  const int64_t row_bytes = p.k_ss * 2;
   const char* kbase = uniform_ptr(p.k + kv_head(p, blk));
   const char* vbase = uniform_ptr(p.v + kv_head(p, blk));
-  // Per-lane byte offsets within a tile (row * row_bytes + swizzled chunk) are
-  // loop invariants; the LDS destination of each instruction is wave-uniform.
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  uint32_t koff[kDmaPerWave], voff[kDmaPerWave];
-#pragma unroll
-  for (int j = 0; j < kDmaPerWave; ++j) {
-    const int r = dma_row(j, wave, lane);
-    koff[j] = dma_lane_offset(row_bytes, r, dma_kcol(r, lane));
-    voff[j] = dma_lane_offset(row_bytes, r, dma_vcol(r, lane));
-  }
-  // Rows past the sequence (only in the last, partial tile) are clamped to the
-  // last key: their scores are masked and their V rows meet p = 0.
-  auto issue = [&](const char* base, bool is_v, const uint32_t (&off)[kDmaPerWave], int kt,
-                   uint32_t lds) {
-    if (wave_u >= kDmaWaves) return;
-    const int j0 = kt * kBN;
-    const char* tb = base + (int64_t)j0 * row_bytes;
-    if (j0 + kBN <= p.seq) {
-#pragma unroll
-      for (int j = 0; j < kDmaPerWave; ++j)
-        dma16(tb, off[j], lds + (uint32_t)((j * kDmaWaves + wave_u) * 1024));
-    } else {
-#pragma unroll
-      for (int j = 0; j < kDmaPerWave; ++j) {
-        const int r = dma_row(j, wave, lane);
-        dma16(tb, dma_lane_offset(row_bytes, dma_src_row(p, kt, r), is_v ? dma_vcol(r, lane) : dma_kcol(r, lane)),
-              lds + (uint32_t)((j * kDmaWaves + wave_u) * 1024));
-      }
-    }
-  };
-  auto k_tile = [&](int kt) { return smem + (kt % kRing) * kTileBytes; };
-  auto v_tile = [&](int kt) { return smem + (kRing + kt % kRing) * kTileBytes; };
+  auto k_tile = [&](int kt) { return smem + ring_slot(slot_base, kt) * kTileBytes; };
+  auto v_tile = [&](int kt) { return smem + (kRing + ring_slot(slot_base, kt)) * kTileBytes; };
 
   const int nkt = blk.nkt;
   const int nfree = blk.nfree;   // tiles [0, nfree) need no mask for any row of this workgroup
@@ -380,10 +398,12 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   // iteration kt-2), then computes O += V(kt-1) P(kt-1), S(kt+1) and the softmax of
   // S(kt).  Each DMA has two iterations to land: the barrier that ends iteration
   // kt waits only for the DMAs issued in iteration kt-1 (K(kt+2), V(kt)), which
-  // iteration kt+1 reads.
+  // iteration kt+1 reads.  The prologue issues the first tiles the previous block
+  // did not prefetch; the wait below covers both.
 #pragma unroll
-  for (int i = 0; i < kPrologueK; ++i) issue(kbase, false, koff, prologue_k_tile(i, nkt), lds_addr(k_tile(i)));
-  issue(vbase, true, voff, 0, lds_addr(v_tile(0)));
+  for (int i = 0; i < kPrologueK; ++i)
+    if (!prologue_k_prefetched(i, prev_nkt)) issue(kbase, false, koff, prologue_k_tile(i, nkt), lds_addr(k_tile(i)));
+  if (!prologue_v_prefetched(prev_nkt)) issue(vbase, true, voff, 0, lds_addr(v_tile(0)));
   wait_vmcnt<0>();
   __syncthreads();
   floatx4 s[kIT][4];
@@ -393,12 +413,23 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   scores(st, k_tile(0), lane, s);
   __syncthreads();
 
-  // Past the last tile the DMAs fetch the last tile again into a slot that is
-  // no longer read, so every iteration issues the same number of DMAs and the
-  // wait below has a fixed count.
+  // Past the last tile the DMAs fetch the next block's first tiles, or after the
+  // last block the last tile again into a slot that is no longer read, so every
+  // iteration issues the same number of DMAs and the wait below has a fixed count.
+  // (The next block's geometry is worked out only in a block's last iterations.)
   auto fetch = [&](int kt) {
-    issue(kbase, false, koff, k_fetch_tile(kt, nkt), lds_addr(k_tile(kt + 3)));
-    issue(vbase, true, voff, v_fetch_tile(kt, nkt), lds_addr(v_tile(kt + 1)));
+    if (kt + kPrologueK < nkt) {
+      issue(kbase, false, koff, kt + kPrologueK, lds_addr(k_tile(kt + kPrologueK)));
+      issue(vbase, true, voff, kt + 1, lds_addr(v_tile(kt + 1)));
+    } else {
+      const bool has_next = CAUSAL && bid_next < nb_total;
+      const Block nxt = block_of(p, CAUSAL, HPW, has_next ? bid_next : bid, wave);
+      const Fetch kf = k_fetch(kt, nkt, has_next, nxt.nkt);
+      const Fetch vf = v_fetch(kt, nkt, has_next);
+      const int64_t kvn = kv_head(p, nxt);
+      issue(kf.next ? uniform_ptr(p.k + kvn) : kbase, false, koff, kf.tile, lds_addr(k_tile(kt + kPrologueK)));
+      issue(vf.next ? uniform_ptr(p.v + kvn) : vbase, true, voff, vf.tile, lds_addr(v_tile(kt + 1)));
+    }
   };
   // O moves to the running max set by the previous tile's statistics; done
   // before the next O += V P (and at the top of an iteration, so the branch does
@@ -465,8 +496,9 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   }
   rescale(any);
   accumulate_pv(st, v_tile(nkt - 1), pf, lane);
-  // The last fetches (repeats of the last tile into slots no longer read) must
-  // land before the workgroup exits and its LDS is handed to another workgroup.
+  // The last fetches (the next block's first tiles, or after the last block
+  // repeats of the last tile into slots no longer read) must land before the next
+  // block reads them, and before the workgroup exits and its LDS is handed on.
   wait_vmcnt<0>();
 
   // ---- normalise and store: lane holds out[row][d = dt*16 + 4g .. +4]; the
@@ -485,6 +517,9 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
       w[1] = pack2(o[2], o[3]);
       *reinterpret_cast<u32x2*>(op + out_elem(p, row, dt, g)) = w;
     }
+  }
+  slot_base = ring_slot(slot_base, nkt);
+  prev_nkt = nkt;
   }
 }
 
@@ -533,7 +568,8 @@ extern "C" int kda_gqa_fwd_bf16(const kda_bf16* q, const kda_bf16* k, const kda_
                            reinterpret_cast<const uint16_t*>(v), reinterpret_cast<uint16_t*>(out), batch,
                            seq, hq, hkv, scale, out_stride_b, out_stride_s, out_stride_h);
   hipStream_t st = as_stream(stream);
-  const dim3 grid((unsigned)nblocks), block(kThreads);
+  // causal: persistent, one workgroup per CU (or per block, if fewer)
+  const dim3 grid((unsigned)(causal ? std::min<int64_t>(nblocks, device_cu_count()) : nblocks)), block(kThreads);
 #define KDA_GQA_LAUNCH(H)                                                         \
   if (causal)                                                                     \
     hipLaunchKernelGGL((gqa_fwd_kernel<true, H>), grid, block, 0, st, a);         \

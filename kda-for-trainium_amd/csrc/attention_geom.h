@@ -153,14 +153,54 @@ __host__ __device__ __forceinline__ uint32_t dma_vcol(int r, int lane) {
 __host__ __device__ __forceinline__ uint32_t dma_lane_offset(int64_t row_bytes, int r, uint32_t col) {
   return (uint32_t)(r * row_bytes) + col;
 }
-// The key tiles a workgroup's DMAs fetch: before the loop K(0), K(1), K(2) and
-// V(0); iteration kt (0 .. nkt-1) fetches K(kt+3) and V(kt+1).  Past the last
-// tile the last tile is fetched again (into a slot no longer read), so every
-// iteration issues the same number of DMAs.
+// ---- Persistent schedule.  The grid has G = min(blocks, CUs) workgroups;
+// workgroup w runs blocks w, 2G-1-w, 2G+w, 4G-1-w, ... of the longest-first
+// order (a snake over the sorted block lengths, so the totals come out even).
+__host__ __device__ __forceinline__ int sched_block(int k, int w, int grid) {
+  return (k & 1) ? (k + 1) * grid - 1 - w : k * grid + w;
+}
+__host__ __device__ __forceinline__ int total_blocks(const Args& p, int hpw) {
+  const int bm = block_rows(hpw);
+  return ((p.seq + bm - 1) / bm) * p.batch * p.hkv * (p.hq / p.hkv / hpw);
+}
+
+// ---- K/V tile ring.  A workgroup's key tiles, block after block, take the ring
+// slots in turn: tile kt of a block whose first tile sits at ring position
+// `base` uses slot (base + kt) mod kRing, for K and for V alike.
+constexpr int kRing = 4;   // a power of two
+__host__ __device__ __forceinline__ int ring_slot(int base, int kt) { return (base + kt) & (kRing - 1); }
+
+// The key tiles a block's DMAs fetch: before its loop K(0), K(1), K(2) and V(0)
+// (clamped to its last tile); iteration kt (0 .. nkt-1) fetches K(kt+3) and
+// V(kt+1).  Past the block's last tile those DMAs fetch the next block's first
+// tiles (its K(0..2) and V(0)), which that block's prologue then does not
+// issue; after the workgroup's last block they fetch the last tile again (into
+// a slot no longer read).  Every iteration issues the same number of DMAs.
 constexpr int kPrologueK = 3;
-__host__ __device__ __forceinline__ int k_fetch_tile(int kt, int nkt) { return imin(kt + 3, nkt - 1); }
-__host__ __device__ __forceinline__ int v_fetch_tile(int kt, int nkt) { return imin(kt + 1, nkt - 1); }
+struct Fetch {
+  bool next;   // a tile of the next block
+  int tile;    // key tile within its block
+};
+__host__ __device__ __forceinline__ Fetch k_fetch(int kt, int nkt, bool has_next, int nkt_next) {
+  const int j = kt + kPrologueK;
+  if (j < nkt) return Fetch{false, j};
+  if (has_next) return Fetch{true, imin(j - nkt, nkt_next - 1)};
+  return Fetch{false, nkt - 1};
+}
+__host__ __device__ __forceinline__ Fetch v_fetch(int kt, int nkt, bool has_next) {
+  const int j = kt + 1;
+  if (j < nkt) return Fetch{false, j};
+  if (has_next) return Fetch{true, 0};
+  return Fetch{false, nkt - 1};
+}
 __host__ __device__ __forceinline__ int prologue_k_tile(int i, int nkt) { return imin(i, nkt - 1); }
+// Whether prologue tile K(i) was fetched by the previous block's last
+// iterations (prev_nkt: that block's tile count, 0 for a workgroup's first block).
+__host__ __device__ __forceinline__ bool prologue_k_prefetched(int i, int prev_nkt) {
+  return i >= kPrologueK - prev_nkt;
+}
+// V(0) likewise (fetched by the previous block's last iteration).
+__host__ __device__ __forceinline__ bool prologue_v_prefetched(int prev_nkt) { return prev_nkt > 0; }
 
 // Source row of tile row r in key tile kt: rows past the sequence (only in the
 // last, partial tile) are clamped to the last key.

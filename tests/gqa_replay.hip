@@ -1,17 +1,27 @@
-// Host replay of the global memory accesses of the bf16 GQA forward kernel
-// (kda_gqa_fwd_bf16, csrc/attention.hip).  It runs no GPU code: it walks every
-// workgroup, wave and lane of a launch through the geometry functions the kernel
-// computes its addresses with (csrc/attention_geom.h), in the kernel's own
-// schedule, and checks that
+// Host replay of the global memory accesses and the K/V ring schedule of the
+// bf16 GQA forward kernel (kda_gqa_fwd_bf16, csrc/attention.hip).  It runs no GPU
+// code: it walks every workgroup, block, wave and lane of a launch through the
+// geometry and schedule functions the kernel computes its addresses with
+// (csrc/attention_geom.h), in the kernel's own order, and checks that
 //   - every q load (16 bytes) lies inside q, every K/V tile DMA source (16 bytes,
 //     after the clamp of rows past the sequence) inside k or v, and every output
 //     store (8 bytes) inside out;
 //   - no per-lane 32-bit DMA offset wraps (it equals the exact row * row_bytes + chunk);
 //   - every DMA lands inside its 16 KiB LDS tile;
-//   - every output element is stored exactly once.
+//   - every block is run by exactly one workgroup (the persistent schedule), and
+//     every output element is stored exactly once;
+//   - the K/V ring holds the right tile whenever the kernel reads one: the tile of
+//     the right block, fetched at least two iterations earlier or before a full
+//     wait (vmcnt(0)), and no DMA overwrites a slot whose content is still read in
+//     the same or a later iteration.  This covers the prefetch of a block's first
+//     tiles by the previous block's last iterations.
 // Buffers sit at fake base addresses, so only the arithmetic is exercised.
 //
-// usage: gqa_replay B S HQ HKV causal(0/1) layout(bshd/bhsd)
+// usage: gqa_replay B S HQ HKV causal(0/1) layout(bshd/bhsd) [grid [mistake]]
+//   grid: workgroups of the causal (persistent) launch, default min(blocks, 256)
+//   mistake: replay a deliberately wrong schedule, to show the ring checks catch it:
+//     1 = a block's prologue assumes all its first K tiles were prefetched,
+//     2 = the K DMA of iteration kt targets the slot of tile kt+2 instead of kt+3
 // prints "ok ..." and exits 0, or lists the first violations and exits 1.
 #include <cstdio>
 #include <cstdlib>
@@ -44,11 +54,17 @@ void check(const Buf& buf, uint64_t addr, uint64_t n, int block, int wave, int l
     fail(buf.name, "block %lld wave %lld lane %lld out of bounds", block, wave, lane);
 }
 
+// One ring slot of K or V: which tile it holds and when it was fetched / last read.
+struct Slot {
+  int block = -1, tile = -1;
+  long write_step = -1, last_read = -1;
+};
+
 }  // namespace
 
 int main(int argc, char** argv) {
-  if (argc != 7) {
-    std::fprintf(stderr, "usage: %s B S HQ HKV causal layout\n", argv[0]);
+  if (argc < 7 || argc > 9) {
+    std::fprintf(stderr, "usage: %s B S HQ HKV causal layout [grid [mistake]]\n", argv[0]);
     return 2;
   }
   const int64_t B = std::atoll(argv[1]), S = std::atoll(argv[2]), HQ = std::atoll(argv[3]),
@@ -66,75 +82,128 @@ int main(int argc, char** argv) {
                            HQ, HKV, 0.088f, o_sb, o_ss, o_sh);
   const int hpw = heads_per_workgroup(HQ / HKV);
   const int64_t nblocks = grid_blocks(B, S, HQ, HKV);
+  if (nblocks != total_blocks(p, hpw)) fail("blocks", "grid_blocks %lld != total_blocks %lld%lld", nblocks, total_blocks(p, hpw), 0);
+  // the launcher: causal runs min(blocks, CUs) persistent workgroups, non-causal one per block
+  int64_t grid = causal ? (nblocks < 256 ? nblocks : 256) : nblocks;
+  if (argc >= 8 && causal && std::atoll(argv[7]) > 0) grid = std::atoll(argv[7]);
+  const int mistake = argc == 9 ? std::atoi(argv[8]) : 0;
   std::vector<uint8_t> written((size_t)(B * S * HQ * kD / 4), 0);   // per 4-element store
+  std::vector<uint8_t> ran((size_t)nblocks, 0);
   const int64_t row_bytes = p.k_ss * 2;
-  long long n_q = 0, n_dma = 0, n_st = 0;
+  long long n_q = 0, n_dma = 0, n_st = 0, n_reads = 0;
 
-  for (int blk = 0; blk < nblocks; ++blk) {
-    for (int wave = 0; wave < kWaves; ++wave) {
-      const Block g = block_of(p, causal, hpw, blk, wave);
-      // q fragments: rows w0 + it*16 + l16, d chunks dc, lane group g4 = lane >> 4
-      for (int lane = 0; lane < 64; ++lane)
-        for (int it = 0; it < kWaveRows / 16; ++it) {
-          const int row = g.w0 + it * 16 + (lane & 15);
-          if (row >= p.seq) continue;
-          for (int dc = 0; dc < 4; ++dc) {
-            check(q, q.base + 2 * (uint64_t)(q_head(p, g) + q_elem(p, row, dc, lane >> 4)), 16, blk, wave, lane);
-            ++n_q;
-          }
-        }
-      // K/V tile DMAs in the kernel's order (waves below kDmaWaves issue them)
-      if (wave < kDmaWaves) {
-        std::vector<std::pair<int, bool>> tiles;   // (key tile, is V)
-        for (int i = 0; i < kPrologueK; ++i) tiles.push_back({prologue_k_tile(i, g.nkt), false});
-        tiles.push_back({0, true});
-        for (int kt = 0; kt < g.nkt; ++kt) {
-          tiles.push_back({k_fetch_tile(kt, g.nkt), false});
-          tiles.push_back({v_fetch_tile(kt, g.nkt), true});
-        }
-        for (const auto& tv : tiles) {
-          const int kt = tv.first;
-          const bool is_v = tv.second;
-          if (kt < 0 || kt >= g.nkt) fail("schedule", "tile %lld outside 0..%lld (block %lld)", kt, g.nkt - 1, blk);
-          const Buf& buf = is_v ? v : k;
-          const uint64_t tile_base = buf.base + 2 * (uint64_t)kv_head(p, g) + (uint64_t)kt * kBN * row_bytes;
-          for (int j = 0; j < kDmaPerWave; ++j)
-            for (int lane = 0; lane < 64; ++lane) {
-              const int r = dma_row(j, wave, lane);
-              const int src = dma_src_row(p, kt, r);
-              const uint32_t col = is_v ? dma_vcol(r, lane) : dma_kcol(r, lane);
-              const uint32_t off = dma_lane_offset(row_bytes, src, col);
-              if ((int64_t)off != src * row_bytes + col)
-                fail("dma offset", "32-bit offset wraps: row %lld row_bytes %lld block %lld", src, row_bytes, blk);
-              check(buf, tile_base + off, 16, blk, wave, lane);
-              const int64_t lds = (int64_t)(j * kDmaWaves + wave) * 1024 + 16 * lane;
-              if (lds < 0 || lds + 16 > kTileBytes) fail("lds", "DMA lands at %lld (wave %lld lane %lld)", lds, wave, lane);
-              ++n_dma;
-            }
-        }
-      }
-      // output stores: rows w0 + it*16 + l16, d tiles dt
-      for (int lane = 0; lane < 64; ++lane)
-        for (int it = 0; it < kWaveRows / 16; ++it) {
-          const int row = g.w0 + it * 16 + (lane & 15);
-          if (row >= p.seq) continue;
-          for (int dt = 0; dt < kD / 16; ++dt) {
-            const int64_t e = out_head(p, g) + out_elem(p, row, dt, lane >> 4);
-            check(o, o.base + 2 * (uint64_t)e, 8, blk, wave, lane);
-            if (e % 4 == 0 && e >= 0 && e / 4 < (int64_t)written.size()) ++written[(size_t)(e / 4)];
-            else fail("store", "element %lld not a 4-aligned output index (block %lld wave %lld)", e, blk, wave);
-            ++n_st;
-          }
+  // global source checks of one DMA (all lanes of the issuing waves)
+  auto dma = [&](int bid, bool is_v, int kt) {
+    const Buf& buf = is_v ? v : k;
+    for (int wave = 0; wave < kDmaWaves; ++wave) {
+      const Block g = block_of(p, causal, hpw, bid, wave);
+      if (kt < 0 || kt >= g.nkt) fail("schedule", "tile %lld outside 0..%lld (block %lld)", kt, g.nkt - 1, bid);
+      const uint64_t tile_base = buf.base + 2 * (uint64_t)kv_head(p, g) + (uint64_t)kt * kBN * row_bytes;
+      for (int j = 0; j < kDmaPerWave; ++j)
+        for (int lane = 0; lane < 64; ++lane) {
+          const int r = dma_row(j, wave, lane);
+          const int src = dma_src_row(p, kt, r);
+          const uint32_t col = is_v ? dma_vcol(r, lane) : dma_kcol(r, lane);
+          const uint32_t off = dma_lane_offset(row_bytes, src, col);
+          if ((int64_t)off != src * row_bytes + col)
+            fail("dma offset", "32-bit offset wraps: row %lld row_bytes %lld block %lld", src, row_bytes, bid);
+          check(buf, tile_base + off, 16, bid, wave, lane);
+          const int64_t lds = (int64_t)(j * kDmaWaves + wave) * 1024 + 16 * lane;
+          if (lds < 0 || lds + 16 > kTileBytes) fail("lds", "DMA lands at %lld (wave %lld lane %lld)", lds, wave, lane);
+          ++n_dma;
         }
     }
+  };
+
+  for (int64_t w = 0; w < grid; ++w) {
+    Slot ring[2][kRing];            // [K, V][slot]
+    long full_wait = -1;            // step of the last vmcnt(0): every earlier write has landed
+    long step = 0;
+    int slot_base = 0, prev_nkt = 0;
+    auto write = [&](int kind, int slot, int bid, int tile) {
+      Slot& s = ring[kind][slot];
+      if (s.last_read >= step)
+        fail("ring", "slot %lld overwritten in step %lld while read in step %lld", slot, step, s.last_read);
+      s = Slot{bid, tile, step, -1};
+      dma(bid, kind == 1, tile);
+    };
+    auto read = [&](int kind, int slot, int bid, int tile) {
+      Slot& s = ring[kind][slot];
+      if (s.block != bid || s.tile != tile)
+        fail("ring", "step %lld reads tile %lld of block %lld but the slot holds another tile", step, tile, bid);
+      if (!(s.write_step + 2 <= step || s.write_step <= full_wait))
+        fail("ring", "step %lld reads a tile fetched in step %lld (not yet landed, block %lld)", step, s.write_step, bid);
+      s.last_read = step;
+      ++n_reads;
+    };
+    for (int kk = 0;; ++kk) {
+      if (!causal && kk > 0) break;
+      const int bid = causal ? sched_block(kk, (int)w, (int)grid) : (int)w;
+      if (bid >= nblocks) break;
+      if (ran[bid]++) fail("schedule", "block %lld run twice (workgroup %lld)%lld", bid, w, 0);
+      const int bid_next = causal ? sched_block(kk + 1, (int)w, (int)grid) : (int)nblocks;
+      const bool has_next = causal && bid_next < nblocks;
+      const Block g0 = block_of(p, causal, hpw, bid, 0);
+      const Block gn = block_of(p, causal, hpw, has_next ? bid_next : bid, 0);
+      const int nkt = g0.nkt;
+      // q loads and output stores of every wave
+      for (int wave = 0; wave < kWaves; ++wave) {
+        const Block g = block_of(p, causal, hpw, bid, wave);
+        for (int lane = 0; lane < 64; ++lane)
+          for (int it = 0; it < kWaveRows / 16; ++it) {
+            const int row = g.w0 + it * 16 + (lane & 15);
+            if (row >= p.seq) continue;
+            for (int dc = 0; dc < 4; ++dc) {
+              check(q, q.base + 2 * (uint64_t)(q_head(p, g) + q_elem(p, row, dc, lane >> 4)), 16, bid, wave, lane);
+              ++n_q;
+            }
+            for (int dt = 0; dt < kD / 16; ++dt) {
+              const int64_t e = out_head(p, g) + out_elem(p, row, dt, lane >> 4);
+              check(o, o.base + 2 * (uint64_t)e, 8, bid, wave, lane);
+              if (e % 4 == 0 && e >= 0 && e / 4 < (int64_t)written.size()) ++written[(size_t)(e / 4)];
+              else fail("store", "element %lld not a 4-aligned output index (block %lld wave %lld)", e, bid, wave);
+              ++n_st;
+            }
+          }
+        if (g.nkt != nkt) fail("schedule", "waves of block %lld disagree on its tile count%lld%lld", bid, 0, 0);
+      }
+      // prologue: the first tiles the previous block did not prefetch, a full
+      // wait, then S(0) reads K(0)
+      for (int i = 0; i < kPrologueK; ++i)
+        if (!(prologue_k_prefetched(i, prev_nkt) || (mistake == 1 && prev_nkt > 0)))
+          write(0, ring_slot(slot_base, i), bid, prologue_k_tile(i, nkt));
+      if (!prologue_v_prefetched(prev_nkt)) write(1, ring_slot(slot_base, 0), bid, 0);
+      full_wait = step;
+      read(0, ring_slot(slot_base, 0), bid, 0);
+      // iterations kt = 0 .. nkt-1 (one step each), then the last O += V P
+      for (int kt = 0; kt < nkt; ++kt) {
+        ++step;
+        const Fetch kf = k_fetch(kt, nkt, has_next, gn.nkt);
+        const Fetch vf = v_fetch(kt, nkt, has_next);
+        write(0, ring_slot(slot_base, kt + (mistake == 2 ? kPrologueK - 1 : kPrologueK)), kf.next ? bid_next : bid,
+              kf.tile);
+        write(1, ring_slot(slot_base, kt + 1), vf.next ? bid_next : bid, vf.tile);
+        if (kt >= 1) read(1, ring_slot(slot_base, kt - 1), bid, kt - 1);   // O += V(kt-1) P(kt-1)
+        if (kt + 1 < nkt) read(0, ring_slot(slot_base, kt + 1), bid, kt + 1);   // S(kt+1)
+      }
+      ++step;
+      read(1, ring_slot(slot_base, nkt - 1), bid, nkt - 1);
+      full_wait = step;   // vmcnt(0) before the stores
+      ++step;             // the barrier at the top of the next block
+      slot_base = ring_slot(slot_base, nkt);
+      prev_nkt = nkt;
+    }
   }
+  for (int64_t b = 0; b < nblocks; ++b)
+    if (ran[(size_t)b] != 1) fail("schedule", "block %lld run %lld times%lld", b, ran[(size_t)b], 0);
   long long never = 0, twice = 0;
-  for (uint8_t w : written) never += (w == 0), twice += (w > 1);
+  for (uint8_t x : written) never += (x == 0), twice += (x > 1);
   if (never || twice) fail("coverage", "%lld output groups never stored, %lld stored more than once (%lld)", never, twice, 0);
   if (g_bad) {
     std::printf("FAIL %ld violations\n", g_bad);
     return 1;
   }
-  std::printf("ok blocks=%lld q_loads=%lld dmas=%lld stores=%lld\n", (long long)nblocks, n_q, n_dma, n_st);
+  std::printf("ok blocks=%lld grid=%lld q_loads=%lld dmas=%lld ring_reads=%lld stores=%lld\n", (long long)nblocks,
+              (long long)grid, n_q, n_dma, n_reads, n_st);
   return 0;
 }

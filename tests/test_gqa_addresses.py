@@ -1,14 +1,21 @@
-"""Host replay of every global access of the bf16 GQA kernel (no GPU).
+"""Host replay of every global access and of the K/V ring schedule of the bf16
+GQA kernel (no GPU).
 
-tests/gqa_replay.hip walks each workgroup, wave and lane of a kda_gqa_fwd_bf16
-launch through the geometry functions the kernel itself computes its addresses
-with (kda-for-trainium_amd/csrc/attention_geom.h), in the kernel's DMA schedule,
-and checks that q loads, K/V tile DMA sources (after the clamp of rows past the
-sequence), LDS destinations and output stores stay inside their buffers, that no
-32-bit DMA offset wraps, and that every output element is stored exactly once.
-Shapes: the causal graded configuration, ragged and partial-tile shapes (B2 S333
-Hq8 Hkv2 among them), every heads-per-workgroup case, both output layouts, and
-the largest kv-head count the launcher accepts, next to the first it refuses."""
+tests/gqa_replay.hip walks each workgroup, block, wave and lane of a
+kda_gqa_fwd_bf16 launch through the geometry and schedule functions the kernel
+itself computes its addresses with (kda-for-trainium_amd/csrc/attention_geom.h),
+in the kernel's DMA schedule, and checks that q loads, K/V tile DMA sources (after
+the clamp of rows past the sequence), LDS destinations and output stores stay
+inside their buffers, that no 32-bit DMA offset wraps, that the persistent
+(causal) schedule runs every block once and every output element is stored
+exactly once, and that every read of the K/V ring finds the right block's tile,
+landed, and is never overtaken by a DMA into its slot -- including the prefetch
+of a block's first tiles by the previous block.
+Shapes: the causal graded configuration (at the launcher's grid and at smaller
+ones, so that workgroups run several blocks), ragged and partial-tile shapes (B2
+S333 Hq8 Hkv2 among them), every heads-per-workgroup case, both output layouts,
+and the largest kv-head count the launcher accepts, next to the first it refuses.
+Two deliberately wrong schedules show that the ring checks fail when they should."""
 import shutil
 import subprocess
 from pathlib import Path
@@ -31,9 +38,10 @@ def replay(tmp_path_factory):
     return exe
 
 
-def run(exe, b, s, hq, hkv, causal, layout="bshd"):
-    r = subprocess.run([str(exe), str(b), str(s), str(hq), str(hkv), str(int(causal)), layout],
-                       capture_output=True, text=True, timeout=120)
+def run(exe, b, s, hq, hkv, causal, layout="bshd", grid=0, mistake=0):
+    r = subprocess.run([str(exe), str(b), str(s), str(hq), str(hkv), str(int(causal)), layout,
+                        str(grid), str(mistake)],
+                       capture_output=True, text=True, timeout=300)
     return r.returncode, r.stdout
 
 
@@ -55,6 +63,28 @@ def test_every_access_in_bounds(replay, b, s, hq, hkv, causal, layout):
     rc, out = run(replay, b, s, hq, hkv, causal, layout)
     print(out)
     assert rc == 0 and out.startswith("ok "), out
+
+
+@pytest.mark.parametrize("b,s,hq,hkv,grid", [
+    (4, 4096, 32, 8, 1),      # one workgroup runs all 2048 blocks
+    (4, 4096, 32, 8, 100),
+    (2, 333, 8, 2, 1),        # blocks of 1 to 6 tiles: prefetch of fewer than 3 tiles
+    (2, 333, 8, 2, 3),
+    (1, 130, 4, 4, 2),        # 1-, 2- and 3-tile blocks
+    (1, 517, 6, 2, 5),
+])
+def test_persistent_schedule_at_other_grids(replay, b, s, hq, hkv, grid):
+    rc, out = run(replay, b, s, hq, hkv, True, grid=grid)
+    print(out)
+    assert rc == 0 and out.startswith("ok "), out
+
+
+@pytest.mark.parametrize("mistake", [1, 2])
+def test_ring_checks_catch_a_wrong_schedule(replay, mistake):
+    """A prologue that skips tiles the previous block did not prefetch, and a K DMA
+    one slot early, are both reported as ring violations."""
+    rc, out = run(replay, 2, 333, 8, 2, True, grid=3, mistake=mistake)
+    assert rc == 1 and "VIOLATION ring" in out, out
 
 
 def test_dma_offsets_at_the_kv_head_limit(replay):
