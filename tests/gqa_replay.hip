@@ -21,7 +21,8 @@
 //   grid: workgroups of the causal (persistent) launch, default min(blocks, 256)
 //   mistake: replay a deliberately wrong schedule, to show the ring checks catch it:
 //     1 = a block's prologue assumes all its first K tiles were prefetched,
-//     2 = the K DMA of iteration kt targets the slot of tile kt+2 instead of kt+3
+//     2 = the K DMA of iteration kt targets the slot of tile kt+2 instead of kt+3,
+//     3 = a block's prologue waits for nothing (no vmcnt(0) after its own DMAs)
 // prints "ok ..." and exits 0, or lists the first violations and exits 1.
 #include <cstdio>
 #include <cstdlib>
@@ -173,7 +174,7 @@ int main(int argc, char** argv) {
         if (!(prologue_k_prefetched(i, prev_nkt) || (mistake == 1 && prev_nkt > 0)))
           write(0, ring_slot(slot_base, i), bid, prologue_k_tile(i, nkt));
       if (!prologue_v_prefetched(prev_nkt)) write(1, ring_slot(slot_base, 0), bid, 0);
-      full_wait = step;
+      if (mistake != 3) full_wait = step;
       read(0, ring_slot(slot_base, 0), bid, 0);
       // iterations kt = 0 .. nkt-1 (one step each), then the last O += V P
       for (int kt = 0; kt < nkt; ++kt) {

@@ -15,7 +15,7 @@ Shapes: the causal graded configuration (at the launcher's grid and at smaller
 ones, so that workgroups run several blocks), ragged and partial-tile shapes (B2
 S333 Hq8 Hkv2 among them), every heads-per-workgroup case, both output layouts,
 and the largest kv-head count the launcher accepts, next to the first it refuses.
-Two deliberately wrong schedules show that the ring checks fail when they should."""
+Three deliberately wrong schedules show that the ring checks fail when they should."""
 import shutil
 import subprocess
 from pathlib import Path
@@ -79,10 +79,11 @@ def test_persistent_schedule_at_other_grids(replay, b, s, hq, hkv, grid):
     assert rc == 0 and out.startswith("ok "), out
 
 
-@pytest.mark.parametrize("mistake", [1, 2])
+@pytest.mark.parametrize("mistake", [1, 2, 3])
 def test_ring_checks_catch_a_wrong_schedule(replay, mistake):
-    """A prologue that skips tiles the previous block did not prefetch, and a K DMA
-    one slot early, are both reported as ring violations."""
+    """A prologue that skips tiles the previous block did not prefetch, a K DMA one
+    slot early, and a prologue that does not wait for its own DMAs are all reported
+    as ring violations."""
     rc, out = run(replay, 2, 333, 8, 2, True, grid=3, mistake=mistake)
     assert rc == 1 and "VIOLATION ring" in out, out
 
