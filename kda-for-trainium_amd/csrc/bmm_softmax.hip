@@ -85,23 +85,30 @@ __device__ __forceinline__ void limbs2(float x, _Float16& h0, _Float16& h1) {
 // rhs [B][K][N] fp32 -> two fp16 limb planes of rhs^T * 2^(kTopExp - e), each
 // [B][N][64] (k padded with zeros up to 64), and tile_scale[b][tile] =
 // 2^(e - kTopExp), where 2^e is the leading power of two of the tile's largest
-// |value|.  One workgroup per (64-column tile, batch).
+// |value|.  One workgroup per (64-column tile, batch): 16-byte loads of the
+// tile's k-rows into LDS, then each thread writes 16 consecutive k of one column
+// as two 16-byte stores per plane (a wave writes 2 KiB contiguous per plane).
 __global__ __launch_bounds__(256) void split_transpose_kernel(const float* __restrict__ rhs,
                                                               _Float16* __restrict__ p0,
                                                               _Float16* __restrict__ p1,
                                                               float* __restrict__ tile_scale, int k,
                                                               int n) {
-  __shared__ float tile[kK][kCols + 1];
+  __shared__ float tile[kK][kCols + 1];   // [k][column], rows padded: conflict-free column reads
   __shared__ float wave_max[4];
   const int n0 = blockIdx.x * kCols;
   const int64_t b = blockIdx.y;
-  const float* src = rhs + b * (int64_t)k * n;
+  const float* src = rhs + b * (int64_t)k * n + n0;
   float mx = 0.f;
-  for (int idx = threadIdx.x; idx < kK * kCols; idx += 256) {
-    const int r = idx / kCols, c = idx % kCols;   // r = k, c = column (coalesced read)
-    const float v = r < k ? src[(int64_t)r * n + n0 + c] : 0.f;
-    tile[r][c] = v;
-    mx = fmaxf(mx, fabsf(v));
+#pragma unroll
+  for (int i = 0; i < kK / 16; ++i) {
+    const int r = (threadIdx.x >> 4) + 16 * i, c = 4 * (threadIdx.x & 15);   // 16 lanes per 256-byte row
+    const floatx4 v = r < k ? *reinterpret_cast<const floatx4*>(src + (int64_t)r * n + c)
+                            : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      tile[r][c + e] = v[e];
+      mx = fmaxf(mx, fabsf(v[e]));
+    }
   }
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
   if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x >> 6] = mx;
@@ -110,14 +117,20 @@ __global__ __launch_bounds__(256) void split_transpose_kernel(const float* __res
   const int e = top_exponent(mx);
   const float sc = pow2(kTopExp - e);
   if (threadIdx.x == 0) tile_scale[b * (n / kCols) + blockIdx.x] = pow2(e - kTopExp);
-  const int64_t base = (b * n + n0) * kK;
-  for (int idx = threadIdx.x; idx < kK * kCols; idx += 256) {
-    const int c = idx / kK, r = idx % kK;         // write k-contiguous
-    _Float16 h0, h1;
-    limbs2(tile[r][c] * sc, h0, h1);
-    const int64_t o = base + (int64_t)c * kK + r;
-    p0[o] = h0;
-    p1[o] = h1;
+  const int c = threadIdx.x >> 2, q = threadIdx.x & 3;   // column, 16-k chunk
+  const int64_t o = (b * n + n0 + c) * kK + 16 * q;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    half8 h0, h1;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      _Float16 a0, a1;
+      limbs2(tile[16 * q + 8 * hh + j][c] * sc, a0, a1);
+      h0[j] = a0;
+      h1[j] = a1;
+    }
+    *reinterpret_cast<half8*>(p0 + o + 8 * hh) = h0;
+    *reinterpret_cast<half8*>(p1 + o + 8 * hh) = h1;
   }
 }
 
