@@ -60,6 +60,23 @@ def test_gqa_small_full_compare(dev, causal, dims):
     assert err < 5e-3
 
 
+@pytest.mark.parametrize("dims", [dict(B=5, S=3000, HQ=16, HKV=2), dict(B=2, S=2048, HQ=24, HKV=8)])
+def test_gqa_causal_persistent_several_blocks_per_workgroup(dev, dims):
+    """Causal launches run one workgroup per CU over more blocks than CUs: 940 blocks
+    with partial last key tiles (8 heads per workgroup), and 384 blocks of one head
+    each (G = 3), so workgroups run several blocks of different lengths and prefetch
+    each next block's first tiles.  Sampled heads against the oracle."""
+    d = oi.draw("gqa_cfg", 13, dims=dict(dims, D=128))
+    out = to_host(ops.gqa(*(to_dev(d[k], dev, BF) for k in ("q", "k", "v")), causal=True))
+    b_n, h_n = dims["B"], dims["HQ"]
+    heads = [(0, 0), (b_n - 1, h_n - 1), (b_n // 2, h_n // 3), (1, h_n // 2 + 1)]
+    want = threaded_heads(lambda bh: oo.gqa(d["q"], d["k"], d["v"], causal=True, heads=[bh])[0], heads)
+    got = np.stack([out[b, :, h, :] for b, h in heads])
+    err = rel_l2(got, want)
+    print(f"gqa persistent {dims} heads={heads} rel_l2={err:.3e}", flush=True)
+    assert err < 5e-3 and np.isfinite(out).all()
+
+
 def test_gqa_bhsd_layout_and_custom_scale(dev):
     d = oi.draw("gqa_cfg", 9, dims=dict(B=1, S=192, HQ=8, HKV=2, D=128))
     qkv = [to_dev(d[k], dev, BF) for k in ("q", "k", "v")]
