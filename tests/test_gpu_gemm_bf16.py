@@ -195,8 +195,8 @@ def test_swiglu_tail_down_launch_ragged_rows_dirty_workspace(dev):
     # M = 300, K = 1024, F = 16896: 264 gate/up tiles of 256x128 on 256 CUs, so the
     # last 512 columns (8 tiles, 4 per row tile) run in one launch with the down
     # GEMM's 8 tiles of 256x256: 8 workgroups compute a tail tile and then h's
-    # first 7936 columns times w_down, parking the fp32 sums; 8 more compute the
-    # remaining 8960 columns, waiting for the tail tiles of their row before its
+    # first 7616 columns times w_down, parking the fp32 sums; 8 more compute the
+    # remaining 9280 columns, waiting for the tail tiles of their row before its
     # last 512 columns and for the parked sums before the epilogue.  The second
     # row tile holds 44 rows.  The workspace starts as 0xff bytes (the flags are
     # cleared by the gate/up launch), a second call gives the same bits, and the
