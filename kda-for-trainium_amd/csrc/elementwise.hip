@@ -31,7 +31,9 @@ __device__ __forceinline__ float silu1(float x) {
 
 __global__ __launch_bounds__(kBlock) void silu_vec_kernel(const floatx4* __restrict__ x,
                                                           floatx4* __restrict__ y, int64_t n4) {
-  const int64_t base = (int64_t)blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
+  const int64_t first = (int64_t)blockIdx.x * (kBlock * kUnroll);
+  const int64_t base = first + threadIdx.x;
+  const auto yw = out_window(y + first, (uint32_t)(min(n4 - first, (int64_t)kBlock * kUnroll) * 16));
   floatx4 v[kUnroll];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
@@ -47,7 +49,7 @@ __global__ __launch_bounds__(kBlock) void silu_vec_kernel(const floatx4* __restr
       r.y = silu1(v[u].y);
       r.z = silu1(v[u].z);
       r.w = silu1(v[u].w);
-      __builtin_nontemporal_store(r, y + i);
+      store_sc1(yw, (uint32_t)((i - first) * 16), r);
     }
   }
 }
@@ -86,7 +88,9 @@ __global__ __launch_bounds__(kAdamBlock) void adamw_vec_kernel(const floatx4* p_
                                                            AdamParams a) {
   // p_out may alias p_in (and m_out/v_out alias m_in/v_in): every element is
   // loaded by the thread that later stores it, and all loads precede all stores.
-  const int64_t base = (int64_t)blockIdx.x * (kAdamBlock * kAdamUnroll) + threadIdx.x;
+  const int64_t first = (int64_t)blockIdx.x * (kAdamBlock * kAdamUnroll);
+  const int64_t base = first + threadIdx.x;
+  const uint32_t wbytes = (uint32_t)(min(n4 - first, (int64_t)kAdamBlock * kAdamUnroll) * 16);
   floatx4 p[kAdamUnroll], g[kAdamUnroll], m[kAdamUnroll], v[kAdamUnroll];
 #pragma unroll
   for (int u = 0; u < kAdamUnroll; ++u) {
@@ -110,10 +114,15 @@ __global__ __launch_bounds__(kAdamBlock) void adamw_vec_kernel(const floatx4* p_
         m[u][j] = mj;
         v[u][j] = vj;
       }
-      __builtin_nontemporal_store(p[u], p_out + i);
-      if (kWriteMoments) {
+      // Store policy measured per form on MI355X: the update in place with its
+      // moments is 4 % slower with SC1 stores than with non-temporal ones (8 %
+      // with SC1 for p alone); the form that writes only a new p is 8 % faster.
+      if constexpr (kWriteMoments) {
+        __builtin_nontemporal_store(p[u], p_out + i);
         __builtin_nontemporal_store(m[u], m_out + i);
         __builtin_nontemporal_store(v[u], v_out + i);
+      } else {
+        store_sc1(out_window(p_out + first, wbytes), (uint32_t)((i - first) * 16), p[u]);
       }
     }
   }
@@ -154,7 +163,8 @@ __global__ __launch_bounds__(kRopeBlock) void rope_vec_kernel(const floatx4* __r
                                                           floatx4* __restrict__ out,
                                                           int64_t half, int64_t s4) {
   const int64_t d = blockIdx.y;
-  const int64_t base = (int64_t)blockIdx.x * (kRopeBlock * kRopeUnroll) + threadIdx.x;
+  const int64_t first = (int64_t)blockIdx.x * (kRopeBlock * kRopeUnroll);
+  const int64_t base = first + threadIdx.x;
   const floatx4* x0p = x + d * s4;
   const floatx4* x1p = x + (d + half) * s4;
   const floatx4* cp = cs + d * s4;
@@ -184,8 +194,10 @@ __global__ __launch_bounds__(kRopeBlock) void rope_vec_kernel(const floatx4* __r
         r0[j] = o0;
         r1[j] = o1;
       }
-      __builtin_nontemporal_store(r0, o0p + i);
-      __builtin_nontemporal_store(r1, o1p + i);
+      const uint32_t wbytes = (uint32_t)(min(s4 - first, (int64_t)kRopeBlock * kRopeUnroll) * 16);
+      const uint32_t off = (uint32_t)((i - first) * 16);
+      store_sc1(out_window(o0p + first, wbytes), off, r0);
+      store_sc1(out_window(o1p + first, wbytes), off, r1);
     }
   }
 }
