@@ -32,10 +32,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t out_window(void* base, uint32_
 }
 // 16 bytes at byte offset `off` (+ the wave-uniform `soff`) of window `w`, with
 // cache policy SC1 (device-scope coherence) instead of the non-temporal policy.
-// Measured on MI355X, same bytes written: SiLU over 64 MiB 6 % faster, over 1 GiB
-// 1.6 % faster, RoPE 9 % faster; plain and SC0 stores were 1-3 % slower than
-// non-temporal ones.  Not a general rule: the small-K bmm's strided 1 GB output
-// ran 22 % slower with it, so each kernel keeps the policy measured best for it.
+// Measured on MI355X with inputs and outputs rotating through more memory than the
+// Infinity Cache holds: SiLU 1.4 % faster (64 MiB and 112 MiB arrays; 1.6 % over
+// 1 GiB); plain and SC0 stores were 1-3 % slower than non-temporal ones.  Not a
+// general rule: RoPE and AdamW ran 1-2 % slower with it, and bmm's strided 1 GB
+// output 22 % slower, so those keep non-temporal stores.
 // A buffer store because no global-store builtin takes a cache policy.
 constexpr int kCpolSc1 = 16;
 __device__ __forceinline__ void store_sc1(__amdgpu_buffer_rsrc_t w, uint32_t off, const floatx4& v,

@@ -88,9 +88,7 @@ __global__ __launch_bounds__(kAdamBlock) void adamw_vec_kernel(const floatx4* p_
                                                            AdamParams a) {
   // p_out may alias p_in (and m_out/v_out alias m_in/v_in): every element is
   // loaded by the thread that later stores it, and all loads precede all stores.
-  const int64_t first = (int64_t)blockIdx.x * (kAdamBlock * kAdamUnroll);
-  const int64_t base = first + threadIdx.x;
-  const uint32_t wbytes = (uint32_t)(min(n4 - first, (int64_t)kAdamBlock * kAdamUnroll) * 16);
+  const int64_t base = (int64_t)blockIdx.x * (kAdamBlock * kAdamUnroll) + threadIdx.x;
   floatx4 p[kAdamUnroll], g[kAdamUnroll], m[kAdamUnroll], v[kAdamUnroll];
 #pragma unroll
   for (int u = 0; u < kAdamUnroll; ++u) {
@@ -114,15 +112,10 @@ __global__ __launch_bounds__(kAdamBlock) void adamw_vec_kernel(const floatx4* p_
         m[u][j] = mj;
         v[u][j] = vj;
       }
-      // Store policy measured per form on MI355X: the update in place with its
-      // moments is 4 % slower with SC1 stores than with non-temporal ones (8 %
-      // with SC1 for p alone); the form that writes only a new p is 8 % faster.
-      if constexpr (kWriteMoments) {
-        __builtin_nontemporal_store(p[u], p_out + i);
+      __builtin_nontemporal_store(p[u], p_out + i);
+      if (kWriteMoments) {
         __builtin_nontemporal_store(m[u], m_out + i);
         __builtin_nontemporal_store(v[u], v_out + i);
-      } else {
-        store_sc1(out_window(p_out + first, wbytes), (uint32_t)((i - first) * 16), p[u]);
       }
     }
   }
@@ -163,8 +156,7 @@ __global__ __launch_bounds__(kRopeBlock) void rope_vec_kernel(const floatx4* __r
                                                           floatx4* __restrict__ out,
                                                           int64_t half, int64_t s4) {
   const int64_t d = blockIdx.y;
-  const int64_t first = (int64_t)blockIdx.x * (kRopeBlock * kRopeUnroll);
-  const int64_t base = first + threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * (kRopeBlock * kRopeUnroll) + threadIdx.x;
   const floatx4* x0p = x + d * s4;
   const floatx4* x1p = x + (d + half) * s4;
   const floatx4* cp = cs + d * s4;
@@ -194,10 +186,8 @@ __global__ __launch_bounds__(kRopeBlock) void rope_vec_kernel(const floatx4* __r
         r0[j] = o0;
         r1[j] = o1;
       }
-      const uint32_t wbytes = (uint32_t)(min(s4 - first, (int64_t)kRopeBlock * kRopeUnroll) * 16);
-      const uint32_t off = (uint32_t)((i - first) * 16);
-      store_sc1(out_window(o0p + first, wbytes), off, r0);
-      store_sc1(out_window(o1p + first, wbytes), off, r1);
+      __builtin_nontemporal_store(r0, o0p + i);
+      __builtin_nontemporal_store(r1, o1p + i);
     }
   }
 }
