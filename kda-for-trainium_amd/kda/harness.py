@@ -83,8 +83,9 @@ def time_op(fn: Callable[[int], Any], warmup: int = 20, iters: int = 100,
     microseconds between a start event and the first wave of the call.
 
     ``fn`` receives the iteration index so a caller can rotate through several
-    input sets (memory-bound operators rotate more than the 256 MB Infinity
-    Cache so repeated calls cannot be served from it).
+    input sets (memory-bound operators rotate inputs of more than twice the
+    256 MB Infinity Cache, and distinct outputs, so repeated calls cannot be
+    served from it).
 
     Warm-up runs at least ``warmup`` calls and at least ``min_warmup_s`` seconds
     of GPU time (at most ``max_warmup`` calls): after an idle spell the MI355X
