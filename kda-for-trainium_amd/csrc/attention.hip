@@ -292,7 +292,7 @@ __device__ __forceinline__ void probs_then_scores(State& st, const uint8_t* k_ld
 // kv head's G query heads are spread over G / HPW workgroups.
 template <bool CAUSAL, int HPW>
 __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
-  __shared__ __align__(1024) uint8_t smem[2 * kRing * kTileBytes];   // K slots, then V slots
+  __shared__ __align__(1024) uint8_t smem[kLdsBytes];   // K slots, V slots, q staging area
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -330,10 +330,15 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
       for (int j = 0; j < kDmaPerWave; ++j)
         dma16(tb, off[j], lds + (uint32_t)((j * kDmaWaves + wave_u) * 1024));
     } else {
+      // The last, partial tile (rare): its clamped offsets are computed here, from a
+      // tile index the compiler may not treat as a constant, so that it does not
+      // precompute them for the whole launch and hold them in registers.
+      int ktv = kt;
+      asm volatile("" : "+s"(ktv));
 #pragma unroll
       for (int j = 0; j < kDmaPerWave; ++j) {
         const int r = dma_row(j, wave, lane);
-        dma16(tb, dma_lane_offset(row_bytes, dma_src_row(p, kt, r), is_v ? dma_vcol(r, lane) : dma_kcol(r, lane)),
+        dma16(tb, dma_lane_offset(row_bytes, dma_src_row(p, ktv, r), is_v ? dma_vcol(r, lane) : dma_kcol(r, lane)),
               lds + (uint32_t)((j * kDmaWaves + wave_u) * 1024));
       }
     }
@@ -348,32 +353,53 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   const int nb_total = total_blocks(p, HPW);
   int slot_base = 0;   // ring position of the current block's first tile
   int prev_nkt = 0;    // tile count of the previous block (0: none)
+  int prev_w0 = 0;     // this wave's first query row in the previous block
   for (int kk = 0; CAUSAL || kk == 0; ++kk) {
   const int bid = sched_block(kk, (int)blockIdx.x, (int)gridDim.x);
   if (bid >= nb_total) break;
-  if (kk > 0) __syncthreads();   // every wave is done with the previous block's LDS
   const Block blk = block_of(p, CAUSAL, HPW, bid, wave);
   const int bid_next = sched_block(kk + 1, (int)blockIdx.x, (int)gridDim.x);
-  const int w0 = blk.w0;                            // this wave's first query row
+  const int w0 = __builtin_amdgcn_readfirstlane(blk.w0);   // this wave's first query row
 
   State st;
   {
-    // Q fragments, scaled by scale*log2(e) and rounded to bf16 once
-    const uint16_t* qp = p.q + q_head(p, blk);
+    // Q fragments, scaled by scale*log2(e) and rounded to bf16 once: a
+    // workgroup's first block loads them from global memory, later blocks read the
+    // rows the previous block staged in LDS.  The staging DMAs were issued before
+    // the previous block's 16 output stores (8 per 16 rows, issued when any of the
+    // 16 rows exists), so waiting for them leaves the stores in flight when row
+    // prev_w0 + 16 exists; otherwise wait for all.
+    // The two paths are kept apart so the LDS path waits for no global load.
+    auto to_frag = [&](const u32x4& raw) {
+      u32x4 w;
 #pragma unroll
-    for (int it = 0; it < kIT; ++it) {
-      const int row = w0 + it * 16 + l16;
+      for (int e = 0; e < 4; ++e)
+        w[e] = pack2(__builtin_bit_cast(float, raw[e] << 16) * p.scale_log2,
+                     __builtin_bit_cast(float, raw[e] & 0xffff0000u) * p.scale_log2);
+      return __builtin_bit_cast(bf16x8, w);
+    };
+    if (CAUSAL && kk > 0) {
+      if (prev_w0 + 16 < p.seq) wait_vmcnt<kIT * kDT>();
+      else wait_vmcnt<0>();
+      const uint8_t* qs = smem + q_stage_offset(slot_base, wave_u);
 #pragma unroll
-      for (int dc = 0; dc < 4; ++dc) {
-        const u32x4 raw = (row < p.seq)
-                              ? *reinterpret_cast<const u32x4*>(qp + q_elem(p, row, dc, g))
-                              : u32x4{0u, 0u, 0u, 0u};
-        u32x4 w;
+      for (int it = 0; it < kIT; ++it) {
+        const bool live = w0 + it * 16 + l16 < p.seq;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          w[e] = pack2(__builtin_bit_cast(float, raw[e] << 16) * p.scale_log2,
-                       __builtin_bit_cast(float, raw[e] & 0xffff0000u) * p.scale_log2);
-        st.qf[it][dc] = __builtin_bit_cast(bf16x8, w);
+        for (int dc = 0; dc < 4; ++dc) {
+          const u32x4 raw = *reinterpret_cast<const u32x4*>(qs + q_stage_pos(it * 16 + l16, dc * 4 + g));
+          st.qf[it][dc] = to_frag(live ? raw : u32x4{0u, 0u, 0u, 0u});
+        }
+      }
+    } else {
+      const uint16_t* qp = p.q + q_head(p, blk);
+#pragma unroll
+      for (int it = 0; it < kIT; ++it) {
+        const int row = w0 + it * 16 + l16;
+#pragma unroll
+        for (int dc = 0; dc < 4; ++dc)
+          st.qf[it][dc] = to_frag((row < p.seq) ? *reinterpret_cast<const u32x4*>(qp + q_elem(p, row, dc, g))
+                                                : u32x4{0u, 0u, 0u, 0u});
       }
     }
 #pragma unroll
@@ -400,11 +426,14 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   // kt waits only for the DMAs issued in iteration kt-1 (K(kt+2), V(kt)), which
   // iteration kt+1 reads.  The prologue issues the first tiles the previous block
   // did not prefetch; the wait below covers both.
+  // When every prologue tile was prefetched (and landed before the previous
+  // block's stores), nothing is awaited here, so those stores stay in flight.
+  const bool all_prefetched = prologue_all_prefetched(prev_nkt);
 #pragma unroll
   for (int i = 0; i < kPrologueK; ++i)
     if (!prologue_k_prefetched(i, prev_nkt)) issue(kbase, false, koff, prologue_k_tile(i, nkt), lds_addr(k_tile(i)));
   if (!prologue_v_prefetched(prev_nkt)) issue(vbase, true, voff, 0, lds_addr(v_tile(0)));
-  wait_vmcnt<0>();
+  if (!all_prefetched) wait_vmcnt<0>();
   __syncthreads();
   floatx4 s[kIT][4];
   bf16x8 pf[kIT][2];
@@ -447,6 +476,16 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
     wait_vmcnt<2 * kDmaPerWave>();
     __syncthreads();
   };
+  // The next block's q rows into LDS, at the start of the last iteration.
+  const bool stage_next = CAUSAL && bid_next < nb_total;
+  auto stage_q = [&]() {
+    const Block nb = block_of(p, CAUSAL, HPW, bid_next, wave);
+    const char* qsrc = uniform_ptr(p.q + q_head(p, nb) + (int64_t)q_src_row0(p, nb.w0) * p.q_ss);
+    const uint32_t qlds = lds_addr(smem + q_stage_offset(ring_slot(slot_base, nkt), wave_u));
+#pragma unroll
+    for (int j = 0; j < kQStageDma; ++j)
+      dma16(qsrc, q_dma_offset(p, nb.w0, q_dma_row(j, lane), q_dma_chunk(j, lane)), qlds + j * 1024);
+  };
 
   // kt = 0: no O update yet.  The first tile sets every row's m to its max
   // (S(0) was computed with m = 0), before S(1) is computed from the new seed.
@@ -454,12 +493,16 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   bool any = false;
   {
     fetch(0);
+    if (nkt == 1 && stage_next) stage_q();
     if (nfree > 0) softmax_test<CAUSAL, false>(p, 0, w0, lane, s, x);
     else softmax_test<CAUSAL, true>(p, 0, w0, lane, s, x);
     softmax_raise<true>(st, s, x, alpha);
     if (nkt > 1) probs_then_scores<false>(st, k_tile(1), lane, s, pf, kf0);
     else softmax_probs(st, s, pf);
-    finish();
+    // iteration 1 reads K(2) and V(0), issued in the prologue (awaited above) or
+    // prefetched by the previous block (landed before its stores)
+    if (all_prefetched) __syncthreads();
+    else finish();
   }
   // Iteration body: block A = O += V(kt-1) P(kt-1) (36 MFMAs) with the row-max
   // test of S(kt); the rare running-max update; block B = the exponentials of
@@ -486,6 +529,7 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   }
   if (kt == nkt - 1 && kt >= 1) {   // last tile: no S(kt+1)
     fetch(kt);
+    if (stage_next) stage_q();
     rescale(any);
     accumulate_pv(st, v_tile(kt - 1), pf, lane);
     any = (kt < nfree) ? softmax_test<CAUSAL, false>(p, kt, w0, lane, s, x)
@@ -499,7 +543,9 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   // The last fetches (the next block's first tiles, or after the last block
   // repeats of the last tile into slots no longer read) must land before the next
   // block reads them, and before the workgroup exits and its LDS is handed on.
-  wait_vmcnt<0>();
+  // The next block's staged q rows (the youngest DMAs) may stay in flight.
+  if (stage_next) wait_vmcnt<kQStageDma>();
+  else wait_vmcnt<0>();
 
   // ---- normalise and store: lane holds out[row][d = dt*16 + 4g .. +4]; the
   // row sum is the sum of the four lanes' parts
@@ -520,6 +566,7 @@ __global__ __launch_bounds__(kThreads, 1) void gqa_fwd_kernel(Args p) {
   }
   slot_base = ring_slot(slot_base, nkt);
   prev_nkt = nkt;
+  prev_w0 = w0;
   }
 }
 
@@ -563,6 +610,13 @@ extern "C" int kda_gqa_fwd_bf16(const kda_bf16* q, const kda_bf16* k, const kda_
     return set_error(KDA_ERR_UNSUPPORTED,
                      "gqa_fwd_bf16: Hkv=%lld kv heads exceed the 32-bit DMA offsets of a key tile",
                      (long long)hkv);
+  // Causal launches stage a wave's next 32 q rows by DMA with 32-bit per-lane
+  // offsets (at most 31 * Hq*D*2 + 240 bytes).
+  if (causal && hq > kMaxHqStaged)
+    return set_error(KDA_ERR_UNSUPPORTED,
+                     "gqa_fwd_bf16: Hq=%lld query heads exceed the 32-bit DMA offsets of the staged q rows "
+                     "(causal: at most %lld)",
+                     (long long)hq, (long long)kMaxHqStaged);
 
   const Args a = make_args(reinterpret_cast<const uint16_t*>(q), reinterpret_cast<const uint16_t*>(k),
                            reinterpret_cast<const uint16_t*>(v), reinterpret_cast<uint16_t*>(out), batch,

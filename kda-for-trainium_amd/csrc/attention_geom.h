@@ -202,6 +202,53 @@ __host__ __device__ __forceinline__ bool prologue_k_prefetched(int i, int prev_n
 // V(0) likewise (fetched by the previous block's last iteration).
 __host__ __device__ __forceinline__ bool prologue_v_prefetched(int prev_nkt) { return prev_nkt > 0; }
 
+// Whether all of a block's prologue tiles (K(0..2), V(0)) were prefetched.
+__host__ __device__ __forceinline__ bool prologue_all_prefetched(int prev_nkt) {
+  return prologue_k_prefetched(0, prev_nkt) && prologue_v_prefetched(prev_nkt);
+}
+
+// ---- q rows of the next block, staged in LDS (causal, persistent).  At the start
+// of a block's last iteration (after its DMAs) each wave DMAs its 32 q rows of the
+// next block into 8 KiB of LDS: waves 0-3 into a 32 KiB area of their own after
+// the rings, waves 4-5 into K slot base+3 and waves 6-7 into V slot base+1, base
+// being the next block's ring position.  Those two slots held the block's K(nkt-1)
+// and V(nkt-3), last read in iteration nkt-2, and no DMA of this block or of the
+// next block's prologue targets them.  The DMAs land during the last iteration, the
+// final O += V P and the stores; issued before the stores, they are awaited at the
+// top of the next block while the stores are still in flight (vmcnt retires in
+// issue order).  The next block reads them before its first ring DMA into those
+// slots (iteration 0, after two barriers).
+constexpr int kQStageBytes = kWaveRows * kD * 2;      // 8 KiB per wave
+constexpr int kQStageDma = kQStageBytes / 1024;       // DMA instructions per wave
+constexpr int kQStageArea = 4 * kQStageBytes;         // waves 0-3, after the K and V rings
+constexpr int kLdsBytes = 2 * kRing * kTileBytes + kQStageArea;   // 160 KiB
+// LDS tile (K slots 0 .. kRing-1, then V slots) and byte offset of a wave's rows.
+// (-1: the staging area after the rings).
+__host__ __device__ __forceinline__ int q_stage_tile(int base, int wave) {
+  return wave < 4 ? -1 : wave < 6 ? ring_slot(base, kPrologueK) : kRing + ring_slot(base, 1);
+}
+__host__ __device__ __forceinline__ int q_stage_offset(int base, int wave) {
+  return wave < 4 ? 2 * kRing * kTileBytes + wave * kQStageBytes
+                  : q_stage_tile(base, wave) * kTileBytes + (wave & 1) * kQStageBytes;
+}
+// Within a wave's 8 KiB: row r (0..31) at r * 256 bytes, its 16-byte chunk c (d =
+// 8c .. 8c+7) at position c ^ (r & 15), conflict-free for the fragment read (16
+// rows, one chunk).  DMA instruction j (0..7) fills rows 4j .. 4j+3: lane ->
+// row 4j + (lane >> 4), position lane & 15.
+__host__ __device__ __forceinline__ int q_stage_pos(int r, int c) { return r * 256 + ((c ^ (r & 15)) << 4); }
+__host__ __device__ __forceinline__ int q_dma_row(int j, int lane) { return 4 * j + (lane >> 4); }
+__host__ __device__ __forceinline__ int q_dma_chunk(int j, int lane) { return (lane & 15) ^ (q_dma_row(j, lane) & 15); }
+// The wave's DMA source: q rows w0 .. w0+31 of head q_head, rows past the sequence
+// clamped to the last one (their results are never stored).  Per-lane 32-bit byte
+// offsets from row min(w0, seq-1), at most 31 * Hq*D*2 + 240 (the launcher bounds Hq).
+__host__ __device__ __forceinline__ int q_src_row0(const Args& p, int w0) { return imin(w0, p.seq - 1); }
+__host__ __device__ __forceinline__ uint32_t q_dma_offset(const Args& p, int w0, int r, int c) {
+  const int row = imin(w0 + r, p.seq - 1);
+  return (uint32_t)((int64_t)(row - q_src_row0(p, w0)) * p.q_ss * 2 + c * 16);
+}
+// Largest Hq whose q DMA offsets fit 32 bits.
+constexpr int64_t kMaxHqStaged = (0xffffffffLL - 240) / ((kWaveRows - 1) * kD * 2);
+
 // Source row of tile row r in key tile kt: rows past the sequence (only in the
 // last, partial tile) are clamped to the last key.
 __host__ __device__ __forceinline__ int dma_src_row(const Args& p, int kt, int r) {

@@ -14,7 +14,10 @@
 //     the right block, fetched at least two iterations earlier or before a full
 //     wait (vmcnt(0)), and no DMA overwrites a slot whose content is still read in
 //     the same or a later iteration.  This covers the prefetch of a block's first
-//     tiles by the previous block's last iterations.
+//     tiles by the previous block's last iterations;
+//   - the next block's q rows, staged by DMA in the last iteration (global source
+//     inside q, no 32-bit offset wrap, LDS inside the wave's own 8 KiB), sit in ring
+//     slots that nothing reads or overwrites until the next block has read them.
 // Buffers sit at fake base addresses, so only the arithmetic is exercised.
 //
 // usage: gqa_replay B S HQ HKV causal(0/1) layout(bshd/bhsd) [grid [mistake]]
@@ -22,7 +25,8 @@
 //   mistake: replay a deliberately wrong schedule, to show the ring checks catch it:
 //     1 = a block's prologue assumes all its first K tiles were prefetched,
 //     2 = the K DMA of iteration kt targets the slot of tile kt+2 instead of kt+3,
-//     3 = a block's prologue waits for nothing (no vmcnt(0) after its own DMAs)
+//     3 = a block's prologue waits for nothing (no vmcnt(0) after its own DMAs),
+//     4 = the q rows of waves 4-5 are staged in K slot base+2 instead of base+3
 // prints "ok ..." and exits 0, or lists the first violations and exits 1.
 #include <cstdio>
 #include <cstdlib>
@@ -60,6 +64,7 @@ struct Slot {
   int block = -1, tile = -1;
   long write_step = -1, last_read = -1;
 };
+constexpr int kQTile = -2;   // a slot holding staged q rows
 
 }  // namespace
 
@@ -91,7 +96,7 @@ int main(int argc, char** argv) {
   std::vector<uint8_t> written((size_t)(B * S * HQ * kD / 4), 0);   // per 4-element store
   std::vector<uint8_t> ran((size_t)nblocks, 0);
   const int64_t row_bytes = p.k_ss * 2;
-  long long n_q = 0, n_dma = 0, n_st = 0, n_reads = 0;
+  long long n_q = 0, n_dma = 0, n_st = 0, n_reads = 0, n_qdma = 0;
 
   // global source checks of one DMA (all lanes of the issuing waves)
   auto dma = [&](int bid, bool is_v, int kt) {
@@ -137,6 +142,38 @@ int main(int argc, char** argv) {
       s.last_read = step;
       ++n_reads;
     };
+    // the next block's q rows: DMA sources and LDS ranges of every wave, and the
+    // two ring slots they occupy (waves 4-5: K slot base+3, waves 6-7: V slot base+1)
+    auto stage = [&](int bid_n, int base_n) {
+      for (int wave = 0; wave < kWaves; ++wave) {
+        const Block g = block_of(p, causal, hpw, bid_n, wave);
+        const uint64_t src0 = q.base + 2 * (uint64_t)(q_head(p, g) + (int64_t)q_src_row0(p, g.w0) * p.q_ss);
+        const int off = q_stage_offset(base_n, wave);
+        if (off < 0 || off + kQStageBytes > kLdsBytes || (wave < 4) != (q_stage_tile(base_n, wave) < 0))
+          fail("q stage", "wave %lld staged at LDS %lld (block %lld)", wave, off, bid_n);
+        for (int j = 0; j < kQStageDma; ++j)
+          for (int lane = 0; lane < 64; ++lane) {
+            const int r = q_dma_row(j, lane), c = q_dma_chunk(j, lane);
+            const int row = imin(g.w0 + r, p.seq - 1);
+            const int64_t exact = (int64_t)(row - q_src_row0(p, g.w0)) * p.q_ss * 2 + c * 16;
+            const uint32_t o32 = q_dma_offset(p, g.w0, r, c);
+            if ((int64_t)o32 != exact) fail("q stage", "32-bit offset wraps: wave %lld row %lld block %lld", wave, row, bid_n);
+            check(q, src0 + o32, 16, bid_n, wave, lane);
+            if (j * 1024 + 16 * lane != q_stage_pos(r, c))   // where the fragment read looks for it
+              fail("q stage", "lane %lld lands where the read does not look (wave %lld, block %lld)", lane, wave, bid_n);
+            ++n_qdma;
+          }
+      }
+      for (int wave = 4; wave < kWaves; wave += 2) {
+        const int t = q_stage_tile(base_n, wave);
+        const int kind = t >= kRing;
+        const int slot = mistake == 4 && wave < 6 ? ring_slot(base_n, 2) : t % kRing;
+        Slot& sl = ring[kind][slot];
+        if (sl.last_read >= step)
+          fail("q stage", "slot %lld staged in step %lld while read in step %lld", slot, step, sl.last_read);
+        sl = Slot{bid_n, kQTile, step, -1};
+      }
+    };
     for (int kk = 0;; ++kk) {
       if (!causal && kk > 0) break;
       const int bid = causal ? sched_block(kk, (int)w, (int)grid) : (int)w;
@@ -147,14 +184,15 @@ int main(int argc, char** argv) {
       const Block g0 = block_of(p, causal, hpw, bid, 0);
       const Block gn = block_of(p, causal, hpw, has_next ? bid_next : bid, 0);
       const int nkt = g0.nkt;
-      // q loads and output stores of every wave
+      // q loads (a workgroup's first block; later ones read q staged in LDS) and
+      // output stores of every wave
       for (int wave = 0; wave < kWaves; ++wave) {
         const Block g = block_of(p, causal, hpw, bid, wave);
         for (int lane = 0; lane < 64; ++lane)
           for (int it = 0; it < kWaveRows / 16; ++it) {
             const int row = g.w0 + it * 16 + (lane & 15);
             if (row >= p.seq) continue;
-            for (int dc = 0; dc < 4; ++dc) {
+            for (int dc = 0; dc < 4 && (!causal || kk == 0); ++dc) {
               check(q, q.base + 2 * (uint64_t)(q_head(p, g) + q_elem(p, row, dc, lane >> 4)), 16, bid, wave, lane);
               ++n_q;
             }
@@ -168,13 +206,24 @@ int main(int argc, char** argv) {
           }
         if (g.nkt != nkt) fail("schedule", "waves of block %lld disagree on its tile count%lld%lld", bid, 0, 0);
       }
+      // staged q rows read at the top of every block after a workgroup's first
+      if (causal && kk > 0) {
+        for (int wave = 4; wave < kWaves; wave += 2) {
+          const int t = q_stage_tile(slot_base, wave);
+          const int kind = t >= kRing, slot = t % kRing;
+          Slot& sl = ring[kind][mistake == 4 && wave < 6 ? ring_slot(slot_base, 2) : slot];
+          if (sl.block != bid || sl.tile != kQTile)
+            fail("q stage", "block %lld wave %lld reads q rows that are not in slot %lld", bid, wave, slot);
+          sl.last_read = step;
+        }
+      }
       // prologue: the first tiles the previous block did not prefetch, a full
-      // wait, then S(0) reads K(0)
+      // wait unless all were prefetched, then S(0) reads K(0)
       for (int i = 0; i < kPrologueK; ++i)
         if (!(prologue_k_prefetched(i, prev_nkt) || (mistake == 1 && prev_nkt > 0)))
           write(0, ring_slot(slot_base, i), bid, prologue_k_tile(i, nkt));
       if (!prologue_v_prefetched(prev_nkt)) write(1, ring_slot(slot_base, 0), bid, 0);
-      if (mistake != 3) full_wait = step;
+      if (mistake != 3 && !prologue_all_prefetched(prev_nkt)) full_wait = step;
       read(0, ring_slot(slot_base, 0), bid, 0);
       // iterations kt = 0 .. nkt-1 (one step each), then the last O += V P
       for (int kt = 0; kt < nkt; ++kt) {
@@ -184,13 +233,14 @@ int main(int argc, char** argv) {
         write(0, ring_slot(slot_base, kt + (mistake == 2 ? kPrologueK - 1 : kPrologueK)), kf.next ? bid_next : bid,
               kf.tile);
         write(1, ring_slot(slot_base, kt + 1), vf.next ? bid_next : bid, vf.tile);
+        if (kt == nkt - 1 && has_next) stage(bid_next, ring_slot(slot_base, nkt));
         if (kt >= 1) read(1, ring_slot(slot_base, kt - 1), bid, kt - 1);   // O += V(kt-1) P(kt-1)
         if (kt + 1 < nkt) read(0, ring_slot(slot_base, kt + 1), bid, kt + 1);   // S(kt+1)
       }
       ++step;
       read(1, ring_slot(slot_base, nkt - 1), bid, nkt - 1);
-      full_wait = step;   // vmcnt(0) before the stores
-      ++step;             // the barrier at the top of the next block
+      full_wait = step;   // every ring DMA has landed before the stores
+      ++step;
       slot_base = ring_slot(slot_base, nkt);
       prev_nkt = nkt;
     }
@@ -204,7 +254,7 @@ int main(int argc, char** argv) {
     std::printf("FAIL %ld violations\n", g_bad);
     return 1;
   }
-  std::printf("ok blocks=%lld grid=%lld q_loads=%lld dmas=%lld ring_reads=%lld stores=%lld\n", (long long)nblocks,
-              (long long)grid, n_q, n_dma, n_reads, n_st);
+  std::printf("ok blocks=%lld grid=%lld q_loads=%lld q_dmas=%lld dmas=%lld ring_reads=%lld stores=%lld\n",
+              (long long)nblocks, (long long)grid, n_q, n_qdma, n_dma, n_reads, n_st);
   return 0;
 }

@@ -119,6 +119,16 @@ def test_gqa_bf16_rejects_kv_heads_beyond_32bit_dma_offsets():
                       0, 0, 0, None)
 
 
+def test_gqa_bf16_causal_rejects_query_heads_beyond_32bit_staging_offsets():
+    """Causal launches stage a wave's next 32 q rows by DMA with 32-bit per-lane
+    offsets (at most 31 * Hq*256 + 240 bytes): Hq = 541201 is refused before any
+    launch (541200 is the largest that fits); the pointers are never dereferenced."""
+    fake = 1 << 20
+    with pytest.raises(ValueError, match="staged q rows"):
+        _lib.call("kda_gqa_fwd_bf16", fake, fake, fake, fake, 1, 64, 541201, 1, 128, 0.088, 1,
+                  0, 0, 0, None)
+
+
 def test_ops_reject_cpu_tensors():
     import torch
     from kda import ops

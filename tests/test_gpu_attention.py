@@ -115,3 +115,28 @@ def test_gqa_group_sizes(dev, causal, hq, hkv):
     err = rel_l2(out, oo.gqa(d["q"], d["k"], d["v"], causal=causal))
     print(f"gqa bf16 Hq={hq} Hkv={hkv} causal={causal} rel_l2={err:.3e}", flush=True)
     assert err < 5e-3
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_gqa_output_8byte_aligned_matches_aligned(dev, causal):
+    """Output rows that are only 8-byte aligned (base 8 bytes past a 16-byte
+    boundary, which the launcher accepts) give the same bits as an aligned output,
+    and nothing is written outside them.  B5 S3000 Hq16 Hkv2: 940 causal blocks, so
+    workgroups run several blocks (staged q rows, stores left in flight)."""
+    import math
+    from kda import _lib
+    b_n, s_n, hq, hkv, d_n = 5, 3000, 16, 2, 128
+    d = oi.draw("gqa_cfg", 17, dims=dict(B=b_n, S=s_n, HQ=hq, HKV=hkv, D=d_n))
+    q, k, v = (to_dev(d[n], dev, BF) for n in ("q", "k", "v"))
+    want = ops.gqa(q, k, v, causal=causal)
+    flat = torch.full((b_n * s_n * hq * d_n + 8,), float("nan"), device=dev, dtype=BF)
+    out = flat[4:4 + b_n * s_n * hq * d_n]                  # 8 bytes past a 16-byte boundary
+    assert out.data_ptr() % 16 == 8
+    _lib.call("kda_gqa_fwd_bf16", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+              b_n, s_n, hq, hkv, d_n, 1.0 / math.sqrt(d_n), 1 if causal else 0,
+              s_n * hq * d_n, hq * d_n, d_n, torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize(dev)
+    got = out.view(b_n, s_n, hq, d_n)
+    print(f"gqa 8-byte aligned output causal={causal}: equal={torch.equal(got, want)}", flush=True)
+    assert torch.equal(got, want)
+    assert torch.isnan(flat[:4]).all() and torch.isnan(flat[-4:]).all()   # nothing outside

@@ -10,12 +10,14 @@ inside their buffers, that no 32-bit DMA offset wraps, that the persistent
 (causal) schedule runs every block once and every output element is stored
 exactly once, and that every read of the K/V ring finds the right block's tile,
 landed, and is never overtaken by a DMA into its slot -- including the prefetch
-of a block's first tiles by the previous block.
+of a block's first tiles by the previous block, and the next block's q rows that
+the last iteration stages in LDS (sources inside q, no offset wrap, slots untouched
+until read).
 Shapes: the causal graded configuration (at the launcher's grid and at smaller
 ones, so that workgroups run several blocks), ragged and partial-tile shapes (B2
 S333 Hq8 Hkv2 among them), every heads-per-workgroup case, both output layouts,
 and the largest kv-head count the launcher accepts, next to the first it refuses.
-Three deliberately wrong schedules show that the ring checks fail when they should."""
+Four deliberately wrong schedules show that the ring checks fail when they should."""
 import shutil
 import subprocess
 from pathlib import Path
@@ -79,11 +81,11 @@ def test_persistent_schedule_at_other_grids(replay, b, s, hq, hkv, grid):
     assert rc == 0 and out.startswith("ok "), out
 
 
-@pytest.mark.parametrize("mistake", [1, 2, 3])
+@pytest.mark.parametrize("mistake", [1, 2, 3, 4])
 def test_ring_checks_catch_a_wrong_schedule(replay, mistake):
     """A prologue that skips tiles the previous block did not prefetch, a K DMA one
-    slot early, and a prologue that does not wait for its own DMAs are all reported
-    as ring violations."""
+    slot early, a prologue that does not wait for its own DMAs, and q rows staged
+    over the next block's prefetched K(2) are all reported as ring violations."""
     rc, out = run(replay, 2, 333, 8, 2, True, grid=3, mistake=mistake)
     assert rc == 1 and "VIOLATION ring" in out, out
 
