@@ -271,6 +271,8 @@ int kda_mamba_f32(const float* delta, const float* u, const float* a, const floa
  * causal != 0 masks keys j > s.  The output element (b,s,h,d) is written at
  * out + b*out_stride_b + s*out_stride_s + h*out_stride_h + d (strides in elements,
  * multiples of 4): BSHD (S*Hq*D, Hq*D, D) or BHSD (Hq*S*D, D, S*D).
+ * KDA_ERR_UNSUPPORTED for Hkv > 266305, and for causal launches with Hq > 541200
+ * (32-bit DMA offsets of a key tile and of a wave's staged q rows).
  * Replaces kernel(v1=q, v2=k, v3=v) of
  * workspaces/gqa_full/runs/gqa_full_v7a_exp_from_psum.py:15-220 (non-causal, BHSD out). */
 int kda_gqa_fwd_bf16(const kda_bf16* q, const kda_bf16* k, const kda_bf16* v, kda_bf16* out,
