@@ -140,3 +140,22 @@ def test_gqa_output_8byte_aligned_matches_aligned(dev, causal):
     print(f"gqa 8-byte aligned output causal={causal}: equal={torch.equal(got, want)}", flush=True)
     assert torch.equal(got, want)
     assert torch.isnan(flat[:4]).all() and torch.isnan(flat[-4:]).all()   # nothing outside
+
+
+@pytest.mark.parametrize("dims", [
+    dict(B=4, S=600, HQ=32, HKV=32),   # G = 1: one head per workgroup, 384 blocks of 256 rows
+    dict(B=4, S=333, HQ=64, HKV=8),    # G = 8: 352 blocks of 32 rows, partial last key tile
+    dict(B=3, S=700, HQ=12, HKV=6),    # G = 2: 396 blocks of 128 rows
+])
+def test_gqa_causal_persistent_every_head(dev, dims):
+    """More causal blocks than CUs at three heads-per-workgroup settings, so every
+    workgroup runs several blocks (prefetched first tiles, q rows staged in LDS,
+    stores left in flight across the block boundary); every head against the oracle."""
+    d = oi.draw("gqa_cfg", 23, dims=dict(dims, D=128))
+    out = to_host(ops.gqa(*(to_dev(d[k], dev, BF) for k in ("q", "k", "v")), causal=True))
+    heads = [(b, h) for b in range(dims["B"]) for h in range(dims["HQ"])]
+    want = threaded_heads(lambda bh: oo.gqa(d["q"], d["k"], d["v"], causal=True, heads=[bh])[0], heads)
+    got = np.stack([out[b, :, h, :] for b, h in heads])
+    err = rel_l2(got, want)
+    print(f"gqa persistent every head {dims} rel_l2={err:.3e}", flush=True)
+    assert err < 5e-3 and np.isfinite(out).all()
