@@ -11,7 +11,8 @@
 // queries).  Causal blocks with the most key tiles are scheduled first, on a
 // persistent grid of one workgroup per CU that runs its blocks in a snake over
 // that order (even totals); a block's last iterations prefetch the next block's
-// first K/V tiles.
+// first K/V tiles and its q rows (into LDS, before the block's output stores, so
+// that the next block's q wait leaves those stores in flight).
 //
 // Staging: K and V tiles of 64 keys go straight from global memory into LDS
 // (global_load_lds_dwordx4, no register staging), each through a 4-slot ring
