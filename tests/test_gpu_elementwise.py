@@ -34,6 +34,20 @@ def test_silu_ragged_and_misaligned(dev, n):
     assert rel_l2(got, oo.silu(x[:n])) < FP32_GATE
 
 
+@pytest.mark.parametrize("n", [4, 1020, 1028, 4096 * 257])
+def test_silu_writes_nothing_past_its_output(dev, n):
+    """The vector path stores through per-workgroup buffer windows: an output that
+    ends inside a workgroup's range (n/4 not a multiple of 256) is written exactly,
+    and the elements after it (and before it) stay as they were."""
+    x = np.random.default_rng(n).normal(size=n).astype(np.float32)
+    buf = torch.full((n + 64,), float("nan"), device=dev)
+    out = buf[32:32 + n]                       # 128-byte aligned start, NaN guards both sides
+    ops.silu(to_dev(x, dev), out=out)
+    torch.cuda.synchronize(dev)
+    assert rel_l2(to_host(out), oo.silu(x)) < FP32_GATE
+    assert torch.isnan(buf[:32]).all() and torch.isnan(buf[32 + n:]).all()
+
+
 def test_silu_extremes_and_empty(dev):
     x = np.array([0.0, -0.0, 88.0, -88.0, 100.0, -100.0, 1e-30, -1e30, 3.0, -3.0, 0.5, -0.5],
                  dtype=np.float32)
