@@ -609,22 +609,30 @@ __device__ __forceinline__ void park_acc(floatx4* tile, const floatx4 (&acc)[NB]
       for (int j = 0; j < TN; ++j) w[((b * TM + i) * TN + j) * 64] = acc[b][i][j];
 }
 
-// The parked values are added TN accumulators at a time: the compiler barrier
-// keeps every load from being hoisted ahead of the adds, which would hold the
-// parked tile and the accumulators (2 x 128 VGPRs) at once and spill.
+// The parked values are added kParkBatch accumulators at a time: a batch's loads
+// are all issued before its adds, so the wave waits kParkBatch times fewer memory
+// round trips than with one load per add, and the compiler barrier after each
+// batch keeps the next batch's loads from being hoisted ahead of its adds, which
+// would hold the whole parked tile and the accumulators (2 x 128 VGPRs) at once
+// and spill.
+constexpr int kParkBatch = 16;
 template <int NB, int TM, int TN>
 __device__ __forceinline__ void add_parked(const floatx4* tile, floatx4 (&acc)[NB][TM][TN]) {
-  const floatx4* w = tile + (size_t)(threadIdx.x >> 6) * (NB * TM * TN * 64) + (threadIdx.x & 63);
+  constexpr int kN = NB * TM * TN;
+  static_assert(kN % kParkBatch == 0, "parked tile is a whole number of batches");
+  const floatx4* w = tile + (size_t)(threadIdx.x >> 6) * (kN * 64) + (threadIdx.x & 63);
+  floatx4* a = &acc[0][0][0];   // flat (b, i, j) order, as park_acc writes them
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
+  for (int q0 = 0; q0 < kN; q0 += kParkBatch) {
+    floatx4 t[kParkBatch];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    for (int u = 0; u < kParkBatch; ++u) t[u] = w[(q0 + u) * 64];
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        acc[b][i][j] += w[((b * TM + i) * TN + j) * 64];
-        asm volatile("" : "+v"(acc[b][i][j]) :: "memory");   // the sum exists before the next batch
-      }
+    for (int u = 0; u < kParkBatch; ++u) {
+      a[q0 + u] += t[u];
+      asm volatile("" : "+v"(a[q0 + u]) :: "memory");   // the sums exist before the next batch
     }
+  }
 }
 
 __global__ __launch_bounds__(kThreads, 1) void swiglu_tail_down_kernel(SwigluFused f) {
