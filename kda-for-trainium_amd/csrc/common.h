@@ -31,17 +31,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t out_window(void* base, uint32_
   return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)bytes, 0x00020000);
 }
 // 16 bytes at byte offset `off` (+ the wave-uniform `soff`) of window `w`, with
-// cache policy SC1 (device-scope coherence) instead of the non-temporal policy.
+// cache policy SC1 + NT (device-scope coherence, streaming) instead of NT alone.
 // Measured on MI355X with inputs and outputs rotating through more memory than the
-// Infinity Cache holds: SiLU 1.4 % faster (64 MiB and 112 MiB arrays; 1.6 % over
-// 1 GiB); plain and SC0 stores were 1-3 % slower than non-temporal ones.  Not a
-// general rule: RoPE and AdamW ran 1-2 % slower with it, and bmm's strided 1 GB
-// output 22 % slower, so those keep non-temporal stores.
+// Infinity Cache holds, SiLU over 64 MiB and 112 MiB arrays: SC1 alone 1.4 % faster
+// than NT, SC1 + NT another 1.2-1.7 % on the single-call median (0.5 % back to
+// back; SC0 + SC1 + NT the same); plain and SC0 stores were 1-3 % slower than NT.
+// Not a general rule: AdamW ran 1-2 % slower with SC1 or SC1 + NT, RoPE no faster,
+// and bmm's strided 1 GB output 22 % slower with SC1, so those keep NT stores.
 // A buffer store because no global-store builtin takes a cache policy.
+constexpr int kCpolNt = 2;
 constexpr int kCpolSc1 = 16;
-__device__ __forceinline__ void store_sc1(__amdgpu_buffer_rsrc_t w, uint32_t off, const floatx4& v,
-                                          uint32_t soff = 0) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), w, (int)off, (int)soff, kCpolSc1);
+__device__ __forceinline__ void store_sc1_nt(__amdgpu_buffer_rsrc_t w, uint32_t off, const floatx4& v,
+                                             uint32_t soff = 0) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), w, (int)off, (int)soff,
+                                         kCpolSc1 | kCpolNt);
 }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

@@ -49,7 +49,7 @@ __global__ __launch_bounds__(kBlock) void silu_vec_kernel(const floatx4* __restr
       r.y = silu1(v[u].y);
       r.z = silu1(v[u].z);
       r.w = silu1(v[u].w);
-      store_sc1(yw, (uint32_t)((i - first) * 16), r);
+      store_sc1_nt(yw, (uint32_t)((i - first) * 16), r);
     }
   }
 }
