@@ -621,7 +621,7 @@ __device__ __forceinline__ void add_parked(const floatx4* tile, floatx4 (&acc)[N
   constexpr int kN = NB * TM * TN;
   static_assert(kN % kParkBatch == 0, "parked tile is a whole number of batches");
   const floatx4* w = tile + (size_t)(threadIdx.x >> 6) * (kN * 64) + (threadIdx.x & 63);
-  floatx4* a = &acc[0][0][0];   // flat (b, i, j) order, as park_acc writes them
+  // parked value q is accumulator (b, i, j) with q = (b * TM + i) * TN + j, as park_acc writes them
 #pragma unroll
   for (int q0 = 0; q0 < kN; q0 += kParkBatch) {
     floatx4 t[kParkBatch];
@@ -629,8 +629,9 @@ __device__ __forceinline__ void add_parked(const floatx4* tile, floatx4 (&acc)[N
     for (int u = 0; u < kParkBatch; ++u) t[u] = w[(q0 + u) * 64];
 #pragma unroll
     for (int u = 0; u < kParkBatch; ++u) {
-      a[q0 + u] += t[u];
-      asm volatile("" : "+v"(a[q0 + u]) :: "memory");   // the sums exist before the next batch
+      const int q = q0 + u, b = q / (TM * TN), i = (q / TN) % TM, j = q % TN;
+      acc[b][i][j] += t[u];
+      asm volatile("" : "+v"(acc[b][i][j]) :: "memory");   // the sums exist before the next batch
     }
   }
 }
