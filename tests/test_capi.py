@@ -129,6 +129,29 @@ def test_gqa_bf16_causal_rejects_query_heads_beyond_32bit_staging_offsets():
                   0, 0, 0, None)
 
 
+def test_header_is_strict_c99(tmp_path):
+    """include/kda.h compiles as ISO C99 on its own, warnings as errors."""
+    src = tmp_path / "use_header.c"
+    src.write_text('#include "kda.h"\nint main(void) { return kda_version() == 100 ? 0 : 1; }\n')
+    subprocess.run(["gcc", "-std=c99", "-pedantic", "-Wall", "-Wextra", "-Werror", "-fsyntax-only",
+                    f"-I{ROOT / 'include'}", str(src)], check=True)
+
+
+def test_c_host_program_validation(tmp_path):
+    """The C99 host program (tests/c_host/silu_host.c), compiled with the C
+    compiler and linked against libkda.so and the HIP runtime, gets the status codes
+    and messages of failed validation from C; no GPU is touched."""
+    import __graft_entry__ as entry
+    exe = tmp_path / "silu_host"
+    cmd = [str(exe) if a == str(entry.C_HOST / "silu_host") else a for a in entry.C_HOST_BUILD]
+    cmd = [a.replace("$ORIGIN/../../kda-for-trainium_amd/kda", str(_lib.LIB_PATH.parent)) for a in cmd]
+    subprocess.run(cmd, check=True)
+    r = subprocess.run([str(exe), "--validate"], capture_output=True, text=True,
+                       env={**__import__("os").environ, "HIP_VISIBLE_DEVICES": ""})
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "rc=1 msg='silu: n=-1 < 0'" in r.stdout and "rc=0 msg=''" in r.stdout
+
+
 def test_ops_reject_cpu_tensors():
     import torch
     from kda import ops
