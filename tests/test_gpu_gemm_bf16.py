@@ -224,3 +224,58 @@ def test_swiglu_ragged(dev, dims):
     err = rel_l2(to_host(got), oo.swiglu(**d))
     print(f"swiglu {dims} rel_l2={err:.3e}", flush=True)
     assert err < 5e-3
+
+
+# ---- launches of more than one round of tiles (more tiles than the device's 256
+# CUs), with a partial last row (and column) of tiles.  Rows are independent and
+# every tile is computed in the same k order, so the first 4096 rows of a 4300-row
+# product (17 x 16 tiles of 256 x 256, the last row of tiles partial) must equal,
+# bit for bit, the 4096-row product (16 x 16 tiles); K from two 32-deep k-tiles up.
+MULTI_ROUND_K = [64, 96, 256]
+
+
+@pytest.mark.parametrize("k", MULTI_ROUND_K)
+def test_matmul_bf16_multi_round_rows_match_one_round(dev, k):
+    rng = np.random.default_rng(k)
+    a, b = _bf16_normal(rng, (4300, k)), _bf16_normal(rng, (k, 4096))
+    ta, tb = to_dev(a, dev, BF), to_dev(b, dev, BF)
+    big = ops.matmul(ta, tb)
+    ref = ops.matmul(ta[:4096].contiguous(), tb)
+    assert torch.equal(big[:4096], ref), f"K={k}: rows of the 4300-row product differ from the 4096-row one"
+    err = rel_l2(to_host(big), oo.matmul(a, b))
+    print(f"matmul_bf16 4300x{k}x4096 rel_l2={err:.3e}", flush=True)
+    assert err < 4e-3
+
+
+@pytest.mark.parametrize("k", MULTI_ROUND_K)
+def test_rmsnorm_matmul_multi_round_rows_match_one_round(dev, k):
+    d = oi.draw("rmsnorm_matmul_cfg", 8, dims=dict(M=4300, K=k, N=4096))
+    x, w, g = to_dev(d["x"], dev, BF), to_dev(d["w"], dev, BF), to_dev(d["gamma"], dev, BF)
+    big = ops.rmsnorm_matmul(x, w, gamma=g, eps=d["eps"])
+    ref = ops.rmsnorm_matmul(x[:4096].contiguous(), w, gamma=g, eps=d["eps"])
+    assert torch.equal(big[:4096], ref), f"K={k}: rows of the 4300-row product differ from the 4096-row one"
+    err = rel_l2(to_host(big), oo.rmsnorm_matmul_gamma(**d))
+    print(f"rmsnorm_matmul 4300x{k}x4096 rel_l2={err:.3e}", flush=True)
+    assert err < 5e-3
+
+
+@pytest.mark.parametrize("dims", [dict(M=4100, K=128, N=4104), dict(M=4352, K=64, N=4360)])
+def test_residual_rmsnorm_multi_round_ragged(dev, dims):
+    """Both residual forms over more than one round of tiles, the last row and
+    column of tiles partial."""
+    for case, fn, ref in (("add_rmsnorm_matmul_cfg", ops.add_rmsnorm_matmul, oo.add_rmsnorm_matmul),
+                          ("matmul_add_rmsnorm_cfg", ops.matmul_add_rmsnorm, oo.matmul_add_rmsnorm)):
+        d = oi.draw(case, 9, dims=dims)
+        err = rel_l2(to_host(fn(*_residual_args(d, dev))), ref(**d))
+        print(f"{case} {dims} rel_l2={err:.3e}", flush=True)
+        assert err < 5e-3
+
+
+def test_swiglu_multi_round_gate_up(dev):
+    """2100 rows, F = 4096: the gate/up launch has 9 x 32 = 288 tiles of 256 x 128
+    (more than one round, the last row of tiles partial); the down GEMM is one round."""
+    d = oi.draw("swiglu_cfg", 10, dims=dict(M=2100, K=1024, F=4096))
+    got = ops.swiglu(*(to_dev(d[k], dev, BF) for k in ("x", "w_up", "w_down", "w_gate")))
+    err = rel_l2(to_host(got), oo.swiglu(**d))
+    print(f"swiglu 2100x1024x4096 rel_l2={err:.3e}", flush=True)
+    assert err < 5e-3
