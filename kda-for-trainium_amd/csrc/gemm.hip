@@ -1094,7 +1094,7 @@ __global__ __launch_bounds__(kRowThreads) void rms_split_f32_kernel(
   __syncthreads();
   float t = 0.f;
 #pragma unroll
-  for (int w = 0; w < kRowThreads / 64; ++w) t += part[w];
+  for (int i = 0; i < kRowThreads / 64; ++i) t += part[i];
   const float rms = sqrtf(t + eps);
   u32x2* hr = reinterpret_cast<u32x2*>(hi + (int64_t)row * k);
   u32x2* lr = reinterpret_cast<u32x2*>(lo + (int64_t)row * k);
