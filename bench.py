@@ -21,7 +21,6 @@ from __future__ import annotations
 import argparse
 import collections
 import json
-import math
 import os
 import sys
 import time

@@ -1,5 +1,4 @@
 """Shared pytest setup: import paths, the `gpu` marker, GPU helpers."""
-import os
 import sys
 from pathlib import Path
 

@@ -5,7 +5,6 @@ index, transposed operand): library routines computed in float64 (torch CPU),
 closed forms, invariants, brute force on tiny inputs, and the known answers the
 reference's own files hold.  CPU only.
 """
-import math
 
 import numpy as np
 import pytest
