@@ -335,8 +335,8 @@ def _rel_l2(got, want):
 def nki_cpu_baseline(name, dev, reps=3):
     """The oracle (numpy) forward of an NKIBench op on this host -- bmm_softmax and
     bmm on 2 of the 16 batches, gqa_full on 2 of the 16 query heads, scaled x8 --
-    and, as the checker, the relative-L2 of the GPU output on the same seed-0
-    inputs.  Returns (ms, sample description, rel_l2)."""
+    and, to check the GPU output, its relative-L2 against the oracle on the same
+    seed-0 inputs.  Returns (ms, sample description, rel_l2)."""
     import torch
     from kda import ops
     from oracle import inputs as oi
@@ -367,8 +367,8 @@ def nki_cpu_baseline(name, dev, reps=3):
 
 def cpu_baseline(name, dev, reps=3):
     """Times the numpy reference forward (the oracle) on this host on a bounded
-    sample scaled linearly to the full configuration, and, as the checker, runs the
-    GPU operator on the same seed-0 sample inputs and compares.
+    sample scaled linearly to the full configuration, and, to check the GPU operator,
+    runs it on the same seed-0 sample inputs and compares.
     Returns (ms, sample description, rel_l2 of the GPU output)."""
     import torch
     from kda import ops
